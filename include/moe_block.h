@@ -1,0 +1,216 @@
+/*
+ * moe_block.h -- C-ABI of the MI355X (gfx950) routed-expert MoE block.
+ *
+ * This is the drop-in boundary for the reference's MoE-block hot path: the
+ * work that moe-serv's ggml backend does behind GGML_OP_MUL_MAT_ID
+ * (moe-serv/src/moe_backend.cpp:413-484 dispatching to
+ * moe-serv/src/moe_tp.h:711-790).  A ggml-backend adapter, the nano-glm
+ * moe-server, or a Python/ctypes caller sits on top of these entry points.
+ *
+ * Conventions
+ *  - Every entry point returns a moe_status (0 = MOE_OK, negative = error);
+ *    no C++ exception crosses this boundary.  On error the context keeps a
+ *    message readable with moe_ctx_last_error().
+ *  - A caller that gets an error other than MOE_ERR_INVALID_ARG runs the
+ *    block on its CPU path instead: the reference's rule is "every fall-back
+ *    is to the CPU, never a skip" (moe_backend.cpp:436-445, moe_tp.h:714-724).
+ *  - Pointers named *_dev are device pointers (HBM); *_host are host memory.
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *  - Weight bytes are ggml block_mxfp4: 17-byte blocks {uint8 e; uint8 qs[16]}
+ *    along the reduction dimension; element j of a block is qs[j] & 0xF and
+ *    element j+16 is qs[j] >> 4; value = kvalue(nibble) * 2^(e-128) with
+ *    kvalues = {0,1,2,3,4,6,8,12,-0,-1,-2,-3,-4,-6,-8,-12}
+ *    (moe-serv/src/moe_tp.h:229-233, hip-moe/src/main.hip:44-57).
+ *  - One context owns one GPU.  Calls on one context are not thread-safe
+ *    (the reference's backend state is process-global singletons,
+ *    moe_backend.cpp:58-62, driven by one scheduler thread).
+ */
+#ifndef MOE_BLOCK_H
+#define MOE_BLOCK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MOE_BLOCK_ABI_VERSION 1
+
+typedef struct moe_ctx moe_ctx;
+typedef struct moe_graph moe_graph;
+
+typedef enum {
+  MOE_OK = 0,
+  MOE_ERR_INVALID_ARG = -1,   /* caller bug: bad pointer, shape or id       */
+  MOE_ERR_HIP = -2,           /* a HIP runtime call failed                  */
+  MOE_ERR_OUT_OF_BUDGET = -3, /* layer does not fit the residency budget    */
+  MOE_ERR_UNSUPPORTED = -4,   /* shape the kernels do not handle            */
+  MOE_ERR_NOT_RESIDENT = -5,  /* layer id has no weights on the device      */
+  MOE_ERR_NO_DEVICE = -6,     /* no usable gfx950 device                    */
+  MOE_ERR_INJECTED = -7       /* failure forced by MOE_BLOCK_INJECT         */
+} moe_status;
+
+/* Router score functions (glm_dsa/moe_block.h:51-53 sigmoid;
+ * deepseek4/moe_block.h:108 sqrt(softplus); softmax as llama.cpp). */
+enum { MOE_ROUTE_SOFTMAX = 0, MOE_ROUTE_SIGMOID = 1, MOE_ROUTE_SQRT_SOFTPLUS = 2 };
+
+/* moe_forward flags */
+enum {
+  /* out is [T][k][H]: the per-slot rows already multiplied by the router
+   * weight (the MUL node of the reference's split, moe_tp.h:754-776); no
+   * slot sum and no shared expert.  Default: out is [T][H], the slot rows
+   * summed in slot order ((y0+y1)+y2)+... plus the shared expert. */
+  MOE_FWD_PER_SLOT = 1u << 0,
+  /* Skip the shared expert even if the layer has one. */
+  MOE_FWD_NO_SHARED = 1u << 1
+};
+
+/* Shape of one MoE layer (moe_tp.h:494-545 reads the same numbers off the
+ * ggml split: K = hidden, INTER = ffn, SLOTS = n_used). */
+typedef struct {
+  int32_t hidden;     /* H: reduction dim of gate/up, output rows of down */
+  int32_t ffn;        /* F: expert FFN width                               */
+  int32_t n_expert;   /* E: routed experts                                 */
+  int32_t n_used;     /* k: experts per token                              */
+  int32_t has_shared; /* 1: one always-on shared expert of the same shape  */
+  float clamp;        /* SwiGLU limit L (> 1e-6 enables: up in [-L, L],
+                         gate <= L, before SiLU; deepseek4/moe_block.h:183-190) */
+} moe_layer_desc;
+
+/* ---- context ------------------------------------------------------------- */
+
+/* Open device `device`.  budget_bytes caps the expert bytes this context may
+ * keep resident (0 = every upload fails with MOE_ERR_OUT_OF_BUDGET, the
+ * analogue of MOESERV_TP_BUDGET_MB=0; UINT64_MAX = no cap).
+ * Replaces moe_tp_init (moe-serv/src/moe_tp.h:392-491). */
+moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx **out);
+void moe_ctx_destroy(moe_ctx *ctx);
+const char *moe_ctx_last_error(const moe_ctx *ctx);
+const char *moe_status_str(moe_status s);
+uint64_t moe_ctx_budget_left(const moe_ctx *ctx);
+
+/* Pre-size the per-call scratch for up to max_tokens tokens per call on
+ * layers of this shape, so that later moe_forward / graph capture calls do
+ * no allocation (moe_tp_set_dims, moe_tp.h:494-545, fixes its scratch the
+ * same way from the first call). */
+moe_status moe_ctx_reserve(moe_ctx *ctx, const moe_layer_desc *desc, int max_tokens);
+
+/* ---- residency ----------------------------------------------------------- */
+
+/* Make a layer resident: copy the ggml MXFP4 tensors from host memory and
+ * repack them on the device.  gate/up are [E][F][H/32] blocks, down is
+ * [E][H][F/32] blocks, the shared expert's are [F][H/32], [F][H/32],
+ * [H][F/32] (NULL when desc->has_shared == 0).  Replaces
+ * moe_tp_setup_layer (moe_tp.h:551-707) and moe_mirror_upload
+ * (moe-serv/src/moe_mirror.h:68-119). */
+moe_status moe_layer_upload(moe_ctx *ctx, int layer, const moe_layer_desc *desc,
+                            const void *gate_host, const void *up_host,
+                            const void *down_host, const void *sh_gate_host,
+                            const void *sh_up_host, const void *sh_down_host);
+
+/* Make a layer resident with synthetic weights generated on the device by
+ * the counter-based generator (seed, layer, tensor, expert, block) with
+ * E8M0 exponents uniform in [e_lo, e_lo + e_span).  Tensor ids: 0 gate,
+ * 1 up, 2 down, 3/4/5 shared gate/up/down.  No counterpart in the
+ * reference (its probes quantize random floats on the host,
+ * moe-serv/src/moe_probe_custom.cpp:679-696); it exists so that 40 layers
+ * (240 GB) can be made resident without a host copy. */
+moe_status moe_layer_generate(moe_ctx *ctx, int layer, const moe_layer_desc *desc,
+                              uint64_t seed, int e_lo, int e_span);
+
+/* Read one expert matrix back in ggml block layout (inverse of the device
+ * repack), into host memory of rows*(K/32)*17 bytes.  expert = E selects
+ * the shared expert.  For round-trip tests. */
+moe_status moe_layer_read_blocks(moe_ctx *ctx, int layer, int tensor, int expert,
+                                 void *out_host);
+
+/* Free a layer's device memory and return its bytes to the budget
+ * (moe_tp_free, moe_tp.h:356-390). */
+moe_status moe_layer_release(moe_ctx *ctx, int layer);
+
+/* Device bytes held by a layer (weights only). */
+moe_status moe_layer_bytes(const moe_ctx *ctx, int layer, uint64_t *bytes);
+
+/* ---- per call ------------------------------------------------------------ */
+
+/* Router: logits [T][E] f32 -> ids [T][k] i32, wts [T][k] f32.  Scores are
+ * softmax / sigmoid / sqrt(softplus) of the logits; bias [E] (or NULL) is
+ * added for selection only; top-k descending, ties to the lower expert id;
+ * weights are the unbiased scores of the selected experts; if norm, divided
+ * by max(sum, 2^-14); if scale is not 0 or 1, multiplied by it
+ * (nano-glm/lib/models/glm_dsa/moe_block.h:48-91). */
+moe_status moe_route(moe_ctx *ctx, const float *logits_dev, const float *bias_dev,
+                     int T, int E, int k, int mode, int norm, float scale,
+                     int32_t *ids_dev, float *wts_dev, void *stream);
+
+/* Token-to-expert grouping of ggml's mul_mat_id: pairs p = t*k + s in
+ * token-major, slot-minor order, stably grouped by expert.
+ * counts[E], offsets[E+1] (exclusive prefix sum), perm[T*k] (grouped row ->
+ * pair), inv[T*k] (pair -> grouped row; may be NULL).  Bit-exact with the
+ * host restatements (nano-glm/apps/moe-server/main.cpp:403-466). */
+moe_status moe_group(moe_ctx *ctx, const int32_t *ids_dev, int T, int k, int E,
+                     int32_t *counts_dev, int32_t *offsets_dev, int32_t *perm_dev,
+                     int32_t *inv_dev, void *stream);
+
+/* The MoE block: x [T][H] f32, ids/wts [T][k] from the router.  Activations
+ * are Q8_0-quantized per 32-block (x before gate/up and the shared expert,
+ * the SwiGLU output before down), weights stay MXFP4; per-block integer
+ * dots, f32 accumulation -- ggml-cpu's MXFP4 x Q8_0 mul_mat_id arithmetic.
+ * Output per `flags` (see MOE_FWD_*).  Replaces moe_tp_compute
+ * (moe_tp.h:711-790) and moe_vk_compute (moe-serv/src/moe_run_vk.h:132-434),
+ * i.e. the device work behind moeserv_backend_graph_compute
+ * (moe_backend.cpp:413-484). */
+moe_status moe_forward(moe_ctx *ctx, int layer, const float *x_dev,
+                       const int32_t *ids_dev, const float *wts_dev, int T,
+                       float *out_dev, uint32_t flags, void *stream);
+
+/* moe_forward from host buffers, synchronous: the reference's per-call
+ * boundary (stage x/ids/wts in, read the result back into the host MUL
+ * node, moe_tp.h:726-777). */
+moe_status moe_forward_host(moe_ctx *ctx, int layer, const float *x_host,
+                            const int32_t *ids_host, const float *wts_host, int T,
+                            float *out_host, uint32_t flags);
+
+/* Router + block in one call: logits [T][E] -> ids/wts (written to the
+ * given device buffers) -> out. */
+moe_status moe_route_forward(moe_ctx *ctx, int layer, const float *x_dev,
+                             const float *logits_dev, const float *bias_dev,
+                             int T, int mode, int norm, float scale,
+                             int32_t *ids_dev, float *wts_dev, float *out_dev,
+                             uint32_t flags, void *stream);
+
+/* ---- hipGraph of a decode step ------------------------------------------- */
+
+/* Capture n_layers consecutive moe_forward calls (layer ids layers[i],
+ * inputs x/ids/wts/out device pointers per layer) into one hipGraph.  The
+ * reference pre-records one command buffer per (layer, die) and replays it
+ * (moe_tp.h:646-701); this is the gfx950 counterpart, for a whole stack.
+ * Needs moe_ctx_reserve for T beforehand (no allocation under capture). */
+moe_status moe_graph_capture(moe_ctx *ctx, int n_layers, const int *layers,
+                             const float *const *x_dev, const int32_t *const *ids_dev,
+                             const float *const *wts_dev, float *const *out_dev,
+                             int T, uint32_t flags, moe_graph **out);
+moe_status moe_graph_launch(moe_graph *g, void *stream);
+void moe_graph_destroy(moe_graph *g);
+
+/* ---- test hooks ---------------------------------------------------------- */
+
+/* Q8_0 of n floats (n % 32 == 0) with the kernels' own quantizer:
+ * qs [n] int8, d [n/32] fp16 bits. */
+moe_status moe_debug_quantize_q8_0(moe_ctx *ctx, const float *x_dev, int n,
+                                   int8_t *qs_dev, uint16_t *d_dev, void *stream);
+
+/* The kernels' 64-lane wave sum applied to 64*n floats (one wave per 64). */
+moe_status moe_debug_wave_sum(moe_ctx *ctx, const float *x_dev, int n_waves,
+                              float *out_dev, void *stream);
+
+/* SwiGLU inputs/outputs of the last moe_forward on this context, for taps:
+ * h [rows][F] f32 before Q8_0, rows = T*k routed pairs in pair order, then
+ * T shared rows.  Copies at most `cap` floats; returns the count in *n. */
+moe_status moe_debug_last_h(moe_ctx *ctx, float *h_host, size_t cap, size_t *n);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* MOE_BLOCK_H */

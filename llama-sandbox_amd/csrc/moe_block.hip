@@ -1,0 +1,674 @@
+// moe_block.hip -- host side of the gfx950 MoE block behind include/moe_block.h.
+//
+// Owns: the device context, per-layer expert residency under a byte budget
+// (moe-serv/src/moe_tp.h:551-707 and moe-serv/src/moe_mirror.h:68-119 are
+// the reference's counterparts), per-call scratch sized once, dispatch of
+// the decode / grouped kernel chains, and hipGraph capture of a stack of
+// layers.  Everything here is plain C++ around hip* calls; no torch.
+#include "../../include/moe_block.h"
+
+#include "device_common.h"
+#include "kernels_decode.h"
+#include "kernels_group.h"
+#include "kernels_weights.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <map>
+#include <string>
+#include <vector>
+
+namespace {
+
+enum { T_GATE = 0, T_UP = 1, T_DOWN = 2 };
+
+struct dev_mat {
+  uint4 *nib = nullptr;   // [E'][R][KB]
+  uint8_t *sc = nullptr;  // [E'][R][KB]
+  int rows = 0, kb = 0;
+};
+
+struct dev_layer {
+  moe_layer_desc d{};
+  int n_mats = 0;      // E + has_shared (the shared expert is expert index E)
+  dev_mat m[3];        // gate, up, down
+  uint64_t bytes = 0;
+};
+
+struct scratch {
+  // sized for (T, H, F, E, k)
+  int T = 0, H = 0, F = 0, E = 0, k = 0;
+  uint32_t *xq = nullptr; float *xd = nullptr;     // [T][H/32][16], [T][H/32]
+  uint32_t *hq = nullptr; float *hd = nullptr;     // [P+T][F/32][16], [P+T][F/32]
+  float *htap = nullptr;                           // [P+T][F]
+  float *y = nullptr;                              // [P+T][H]
+  int32_t *grp = nullptr;                          // grouping workspace
+  size_t grp_words = 0;
+  // host-boundary staging
+  float *x_in = nullptr; int32_t *ids_in = nullptr; float *wts_in = nullptr; float *out_buf = nullptr;
+  size_t out_cap = 0;
+  size_t h_rows = 0;     // rows written to htap by the last forward
+  int last_F = 0;
+};
+
+}  // namespace
+
+struct moe_ctx {
+  int device = 0;
+  uint64_t budget = 0, used = 0;
+  std::map<int, dev_layer> layers;
+  scratch sc;
+  std::string err;
+  int inject = 0;  // bit 0: forward fails, bit 1: budget forced to 0
+  bool capturing = false;
+};
+
+struct moe_graph {
+  moe_ctx *ctx = nullptr;
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+// ---------------------------------------------------------------------------
+static moe_status fail(moe_ctx *c, moe_status s, const char *fmt, ...) {
+  if (c) {
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    c->err = buf;
+  }
+  return s;
+}
+
+#define HIPC(ctx, call)                                                                  \
+  do {                                                                                   \
+    hipError_t e_ = (call);                                                              \
+    if (e_ != hipSuccess)                                                                \
+      return fail((ctx), MOE_ERR_HIP, "%s failed: %s (%s:%d)", #call, hipGetErrorString(e_), \
+                  __FILE__, __LINE__);                                                   \
+  } while (0)
+
+static int ceil_div(long a, long b) { return (int)((a + b - 1) / b); }
+
+// SplitMix64's output function, the host half of the weight generator's key
+// derivation (the device half is mix64 in device_common.h).
+static uint64_t host_mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+static bool desc_ok(const moe_layer_desc *d) {
+  return d && d->hidden > 0 && d->ffn > 0 && d->n_expert > 0 && d->n_used > 0 &&
+         d->hidden % 32 == 0 && d->ffn % 32 == 0 && d->n_used <= d->n_expert &&
+         d->n_used <= 64 && d->n_expert <= MOE_ROUTE_MAX_E && (d->has_shared == 0 || d->has_shared == 1);
+}
+
+static uint64_t layer_bytes(const moe_layer_desc *d) {
+  const uint64_t n = (uint64_t)d->n_expert + (uint64_t)d->has_shared;
+  const uint64_t gu = (uint64_t)d->ffn * (d->hidden / 32) * 17u;
+  const uint64_t dn = (uint64_t)d->hidden * (d->ffn / 32) * 17u;
+  return n * (2 * gu + dn);
+}
+
+// ---------------------------------------------------------------------------
+// scratch
+
+static void scratch_free(scratch &s) {
+  void *ptrs[] = {s.xq, s.xd, s.hq, s.hd, s.htap, s.y, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf};
+  for (void *p : ptrs)
+    if (p) (void)hipFree(p);
+  s = scratch();
+}
+
+static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k) {
+  scratch &s = c->sc;
+  if (s.xq && T <= s.T && H <= s.H && F <= s.F && E <= s.E && k <= s.k) return MOE_OK;
+  if (c->capturing) return fail(c, MOE_ERR_INVALID_ARG, "scratch too small under graph capture; call moe_ctx_reserve first");
+  T = T > s.T ? T : s.T;
+  H = H > s.H ? H : s.H;
+  F = F > s.F ? F : s.F;
+  E = E > s.E ? E : s.E;
+  k = k > s.k ? k : s.k;
+  HIPC(c, hipDeviceSynchronize());
+  scratch_free(s);
+  const size_t P = (size_t)T * k, R = P + T;
+  HIPC(c, hipMalloc(&s.xq, (size_t)T * (H / 32) * 64));
+  HIPC(c, hipMalloc(&s.xd, (size_t)T * (H / 32) * 4));
+  HIPC(c, hipMalloc(&s.hq, R * (F / 32) * 64));
+  HIPC(c, hipMalloc(&s.hd, R * (F / 32) * 4));
+  HIPC(c, hipMalloc(&s.htap, R * F * 4));
+  HIPC(c, hipMalloc(&s.y, R * H * 4));
+  s.grp_words = group_ws_words(T, k, E);
+  HIPC(c, hipMalloc(&s.grp, s.grp_words * 4));
+  HIPC(c, hipMalloc(&s.x_in, (size_t)T * H * 4));
+  HIPC(c, hipMalloc(&s.ids_in, P * 4));
+  HIPC(c, hipMalloc(&s.wts_in, P * 4));
+  s.out_cap = P * H;
+  HIPC(c, hipMalloc(&s.out_buf, s.out_cap * 4));
+  s.T = T; s.H = H; s.F = F; s.E = E; s.k = k;
+  return MOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// context
+
+extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx **out) {
+  if (!out) return MOE_ERR_INVALID_ARG;
+  *out = nullptr;
+  const char *inj = getenv("MOE_BLOCK_INJECT");
+  int inject = 0;
+  if (inj) {
+    if (strstr(inj, "forward")) inject |= 1;
+    if (strstr(inj, "budget")) inject |= 2;
+    if (strstr(inj, "nodevice")) return MOE_ERR_NO_DEVICE;
+  }
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return MOE_ERR_NO_DEVICE;
+  hipDeviceProp_t prop;
+  if (hipGetDeviceProperties(&prop, device) != hipSuccess) return MOE_ERR_NO_DEVICE;
+  if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) return MOE_ERR_NO_DEVICE;
+  if (hipSetDevice(device) != hipSuccess) return MOE_ERR_NO_DEVICE;
+  moe_ctx *c = new moe_ctx;
+  c->device = device;
+  c->budget = (inject & 2) ? 0 : budget_bytes;
+  c->inject = inject;
+  *out = c;
+  return MOE_OK;
+}
+
+extern "C" void moe_ctx_destroy(moe_ctx *c) {
+  if (!c) return;
+  (void)hipSetDevice(c->device);
+  (void)hipDeviceSynchronize();
+  for (auto &kv : c->layers)
+    for (dev_mat &m : kv.second.m) {
+      if (m.nib) (void)hipFree(m.nib);
+      if (m.sc) (void)hipFree(m.sc);
+    }
+  scratch_free(c->sc);
+  delete c;
+}
+
+extern "C" const char *moe_ctx_last_error(const moe_ctx *c) { return c ? c->err.c_str() : ""; }
+
+extern "C" const char *moe_status_str(moe_status s) {
+  switch (s) {
+    case MOE_OK: return "ok";
+    case MOE_ERR_INVALID_ARG: return "invalid argument";
+    case MOE_ERR_HIP: return "HIP runtime error";
+    case MOE_ERR_OUT_OF_BUDGET: return "layer does not fit the residency budget";
+    case MOE_ERR_UNSUPPORTED: return "unsupported shape";
+    case MOE_ERR_NOT_RESIDENT: return "layer not resident";
+    case MOE_ERR_NO_DEVICE: return "no usable gfx950 device";
+    case MOE_ERR_INJECTED: return "injected failure";
+  }
+  return "unknown status";
+}
+
+extern "C" uint64_t moe_ctx_budget_left(const moe_ctx *c) {
+  return c && c->budget > c->used ? c->budget - c->used : 0;
+}
+
+extern "C" moe_status moe_ctx_reserve(moe_ctx *c, const moe_layer_desc *d, int max_tokens) {
+  if (!c || !desc_ok(d) || max_tokens <= 0) return fail(c, MOE_ERR_INVALID_ARG, "moe_ctx_reserve: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  return scratch_reserve(c, max_tokens, d->hidden, d->ffn, d->n_expert, d->n_used);
+}
+
+// ---------------------------------------------------------------------------
+// residency
+
+static moe_status layer_alloc(moe_ctx *c, int layer, const moe_layer_desc *d, dev_layer **out) {
+  if (!desc_ok(d)) return fail(c, MOE_ERR_INVALID_ARG, "layer %d: bad descriptor", layer);
+  if (c->layers.count(layer)) return fail(c, MOE_ERR_INVALID_ARG, "layer %d is already resident", layer);
+  const uint64_t need = layer_bytes(d);
+  if (c->used + need > c->budget || c->used + need < c->used)
+    return fail(c, MOE_ERR_OUT_OF_BUDGET, "layer %d does not fit (%llu MB needed, %llu MB left); CPU fallback",
+                layer, (unsigned long long)(need >> 20),
+                (unsigned long long)((c->budget - c->used) >> 20));
+  HIPC(c, hipSetDevice(c->device));
+  dev_layer L;
+  L.d = *d;
+  L.n_mats = d->n_expert + d->has_shared;
+  const int rows[3] = {d->ffn, d->ffn, d->hidden};
+  const int kbs[3] = {d->hidden / 32, d->hidden / 32, d->ffn / 32};
+  for (int t = 0; t < 3; t++) {
+    const size_t nb = (size_t)L.n_mats * rows[t] * kbs[t];
+    L.m[t].rows = rows[t];
+    L.m[t].kb = kbs[t];
+    hipError_t e1 = hipMalloc(&L.m[t].nib, nb * 16);
+    hipError_t e2 = e1 == hipSuccess ? hipMalloc(&L.m[t].sc, nb) : e1;
+    if (e1 != hipSuccess || e2 != hipSuccess) {
+      for (dev_mat &m : L.m) {
+        if (m.nib) (void)hipFree(m.nib);
+        if (m.sc) (void)hipFree(m.sc);
+      }
+      (void)hipGetLastError();
+      return fail(c, MOE_ERR_OUT_OF_BUDGET, "layer %d: device allocation failed; CPU fallback", layer);
+    }
+  }
+  L.bytes = need;
+  c->used += need;
+  auto it = c->layers.emplace(layer, L).first;
+  *out = &it->second;
+  return MOE_OK;
+}
+
+static void layer_drop(moe_ctx *c, int layer) {
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return;
+  for (dev_mat &m : it->second.m) {
+    if (m.nib) (void)hipFree(m.nib);
+    if (m.sc) (void)hipFree(m.sc);
+  }
+  c->used -= it->second.bytes;
+  c->layers.erase(it);
+}
+
+extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_desc *d,
+                                       const void *gate, const void *up, const void *down,
+                                       const void *sh_gate, const void *sh_up, const void *sh_down) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!gate || !up || !down || (d && d->has_shared && (!sh_gate || !sh_up || !sh_down)))
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_layer_upload: missing tensor");
+  dev_layer *L = nullptr;
+  moe_status st = layer_alloc(c, layer, d, &L);
+  if (st != MOE_OK) return st;
+  // Stage 17-byte blocks through a bounded device buffer, repack on the device.
+  const size_t chunk_blocks = (size_t)1 << 22;  // 68 MiB of blocks per step
+  uint8_t *stage = nullptr;
+  if (hipMalloc(&stage, chunk_blocks * 17) != hipSuccess) {
+    layer_drop(c, layer);
+    return fail(c, MOE_ERR_HIP, "moe_layer_upload: staging allocation failed");
+  }
+  const void *src[3][2] = {{gate, sh_gate}, {up, sh_up}, {down, sh_down}};
+  for (int t = 0; t < 3 && st == MOE_OK; t++) {
+    dev_mat &m = L->m[t];
+    const size_t per_exp = (size_t)m.rows * m.kb;
+    for (int part = 0; part < 1 + d->has_shared && st == MOE_OK; part++) {
+      const uint8_t *host = (const uint8_t *)src[t][part];
+      const size_t nb = part == 0 ? per_exp * d->n_expert : per_exp;
+      const size_t base = part == 0 ? 0 : per_exp * d->n_expert;
+      for (size_t off = 0; off < nb; off += chunk_blocks) {
+        const size_t n = nb - off < chunk_blocks ? nb - off : chunk_blocks;
+        if (hipMemcpy(stage, host + off * 17, n * 17, hipMemcpyHostToDevice) != hipSuccess) {
+          st = fail(c, MOE_ERR_HIP, "moe_layer_upload: host->device copy failed");
+          break;
+        }
+        hipLaunchKernelGGL(k_repack_blocks, dim3(ceil_div((long)n, 256)), dim3(256), 0, 0, stage,
+                           (uint64_t)n, m.nib + base + off, m.sc + base + off);
+      }
+    }
+  }
+  if (st == MOE_OK && hipDeviceSynchronize() != hipSuccess) st = fail(c, MOE_ERR_HIP, "moe_layer_upload: repack failed");
+  (void)hipFree(stage);
+  if (st != MOE_OK) layer_drop(c, layer);
+  return st;
+}
+
+extern "C" moe_status moe_layer_generate(moe_ctx *c, int layer, const moe_layer_desc *d, uint64_t seed,
+                                         int e_lo, int e_span) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (e_lo < 0 || e_span < 1 || e_lo + e_span > 256)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_layer_generate: exponent range");
+  dev_layer *L = nullptr;
+  moe_status st = layer_alloc(c, layer, d, &L);
+  if (st != MOE_OK) return st;
+  for (int t = 0; t < 3; t++) {
+    dev_mat &m = L->m[t];
+    const size_t per_exp = (size_t)m.rows * m.kb;
+    for (int e = 0; e < L->n_mats; e++) {
+      const bool shared = e == d->n_expert;
+      const int tensor = shared ? t + 3 : t;
+      const int expert = shared ? 0 : e;
+      const uint64_t id = ((uint64_t)(uint32_t)layer << 40) ^ ((uint64_t)(uint32_t)tensor << 32) ^
+                          (uint64_t)(uint32_t)expert;
+      const uint64_t key = host_mix64(seed ^ host_mix64(id));
+      hipLaunchKernelGGL(k_generate_blocks, dim3(ceil_div((long)per_exp, 256)), dim3(256), 0, 0, key,
+                         (uint64_t)per_exp, (uint32_t)e_lo, (uint32_t)e_span, m.nib + per_exp * e,
+                         m.sc + per_exp * e);
+    }
+  }
+  if (hipDeviceSynchronize() != hipSuccess) {
+    layer_drop(c, layer);
+    return fail(c, MOE_ERR_HIP, "moe_layer_generate: kernel failed");
+  }
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_layer_read_blocks(moe_ctx *c, int layer, int tensor, int expert, void *out) {
+  if (!c || !out) return MOE_ERR_INVALID_ARG;
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layer);
+  dev_layer &L = it->second;
+  if (tensor < 0 || tensor > 2 || expert < 0 || expert >= L.n_mats)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_layer_read_blocks: tensor/expert out of range");
+  HIPC(c, hipSetDevice(c->device));
+  dev_mat &m = L.m[tensor];
+  const size_t nb = (size_t)m.rows * m.kb;
+  uint8_t *tmp = nullptr;
+  HIPC(c, hipMalloc(&tmp, nb * 17));
+  hipLaunchKernelGGL(k_unpack_blocks, dim3(ceil_div((long)nb, 256)), dim3(256), 0, 0, m.nib + nb * expert,
+                     m.sc + nb * expert, (uint64_t)nb, tmp);
+  hipError_t e = hipMemcpy(out, tmp, nb * 17, hipMemcpyDeviceToHost);
+  (void)hipFree(tmp);
+  if (e != hipSuccess) return fail(c, MOE_ERR_HIP, "moe_layer_read_blocks: copy failed");
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_layer_release(moe_ctx *c, int layer) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!c->layers.count(layer)) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layer);
+  HIPC(c, hipSetDevice(c->device));
+  HIPC(c, hipDeviceSynchronize());
+  layer_drop(c, layer);
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_layer_bytes(const moe_ctx *c, int layer, uint64_t *bytes) {
+  if (!c || !bytes) return MOE_ERR_INVALID_ARG;
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return MOE_ERR_NOT_RESIDENT;
+  *bytes = it->second.bytes;
+  return MOE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// per call
+
+extern "C" moe_status moe_route(moe_ctx *c, const float *logits, const float *bias, int T, int E, int k,
+                                int mode, int norm, float scale, int32_t *ids, float *wts, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!logits || !ids || !wts || T <= 0 || E <= 0 || E > MOE_ROUTE_MAX_E || k <= 0 || k > 64 || k > E ||
+      mode < 0 || mode > 2)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_route: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  hipLaunchKernelGGL(k_route, dim3(T), dim3(256), 0, (hipStream_t)stream, logits, bias, E, k, mode, norm,
+                     scale, ids, wts);
+  HIPC(c, hipGetLastError());
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, int E, int32_t *counts,
+                                int32_t *offsets, int32_t *perm, int32_t *inv, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!ids || !counts || !offsets || !perm || T <= 0 || k <= 0 || E <= 0 || E > MOE_GROUP_MAX_E ||
+      (long)T * k > MOE_GROUP_MAX_PAIRS)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_group: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, counts, offsets,
+                     perm, inv, (int32_t *)nullptr);
+  HIPC(c, hipGetLastError());
+  return MOE_OK;
+}
+
+// The decode chain for T == 1.
+template <int NB>
+static void launch_gu_decode(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *ids,
+                             int k, int shared_expert) {
+  hipLaunchKernelGGL(k_gu_decode<NB>, g, dim3(256), 0, st, L.m[T_GATE].nib, L.m[T_UP].nib, L.m[T_GATE].sc,
+                     L.m[T_UP].sc, s.xq, s.xd, ids, k, shared_expert, L.d.ffn, L.d.hidden / 32, L.d.clamp,
+                     s.hq, s.hd, s.htap);
+}
+
+template <int NB, int RD>
+static void launch_down_decode(int S, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *ids,
+                               const float *wts, int k, int shared_expert, float *out, int per_slot) {
+  hipLaunchKernelGGL((k_down_decode<NB, RD>), dim3(L.d.hidden / RD), dim3(64 * S), 0, st, L.m[T_DOWN].nib,
+                     L.m[T_DOWN].sc, s.hq, s.hd, ids, wts, k, shared_expert, S, L.d.hidden, L.d.ffn / 32, out,
+                     per_slot);
+}
+
+static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
+                                 float *out, uint32_t flags, hipStream_t st) {
+  const moe_layer_desc &d = L.d;
+  const int k = d.n_used;
+  const bool per_slot = flags & MOE_FWD_PER_SLOT;
+  const int S = k + ((d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0);
+  const int KBh = d.hidden / 32, KBf = d.ffn / 32;
+  const int nb_gu = ceil_div(KBh, 64), nb_dn = ceil_div(KBf, 64);
+  if (S > 16 || nb_gu > 6 || nb_dn > 2) return fail(c, MOE_ERR_UNSUPPORTED, "decode: shape outside kernel range");
+  scratch &s = c->sc;
+  hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div(KBh, 256)), dim3(256), 0, st, x, (uint32_t)KBh, s.xq, s.xd,
+                     (int8_t *)nullptr, (uint16_t *)nullptr);
+  const dim3 g(d.ffn / 32, S);
+  switch (nb_gu) {
+    case 1: launch_gu_decode<1>(g, st, L, s, ids, k, d.n_expert); break;
+    case 2: launch_gu_decode<2>(g, st, L, s, ids, k, d.n_expert); break;
+    case 3: launch_gu_decode<3>(g, st, L, s, ids, k, d.n_expert); break;
+    case 4: launch_gu_decode<4>(g, st, L, s, ids, k, d.n_expert); break;
+    case 5: launch_gu_decode<5>(g, st, L, s, ids, k, d.n_expert); break;
+    default: launch_gu_decode<6>(g, st, L, s, ids, k, d.n_expert); break;
+  }
+  s.h_rows = (size_t)S;
+  s.last_F = d.ffn;
+  const int H = d.hidden;
+  const int ps = per_slot ? 1 : 0;
+  if (nb_dn == 1) {
+    if (H % 8 == 0) launch_down_decode<1, 8>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
+    else if (H % 4 == 0) launch_down_decode<1, 4>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
+    else return fail(c, MOE_ERR_UNSUPPORTED, "decode: hidden %% 4 != 0");
+  } else {
+    if (H % 8 == 0) launch_down_decode<2, 8>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
+    else if (H % 4 == 0) launch_down_decode<2, 4>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
+    else return fail(c, MOE_ERR_UNSUPPORTED, "decode: hidden %% 4 != 0");
+  }
+  HIPC(c, hipGetLastError());
+  return MOE_OK;
+}
+
+// The grouped chain for T > 1.
+template <int NB>
+static void launch_gu_grouped(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *offsets,
+                              const int32_t *perm, const int32_t *act, int T, int shared) {
+  hipLaunchKernelGGL(k_gu_grouped<NB>, g, dim3(256), 0, st, L.m[T_GATE].nib, L.m[T_UP].nib, L.m[T_GATE].sc,
+                     L.m[T_UP].sc, s.xq, s.xd, offsets, perm, act, L.d.n_used, T, shared, L.d.n_expert,
+                     L.d.ffn, L.d.hidden / 32, L.d.clamp, s.hq, s.hd, s.htap);
+}
+
+template <int NB, int RD>
+static void launch_down_grouped(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s,
+                                const int32_t *offsets, const int32_t *perm, const int32_t *act, const float *wts,
+                                int T, int shared) {
+  hipLaunchKernelGGL((k_down_grouped<NB, RD>), g, dim3(256), 0, st, L.m[T_DOWN].nib, L.m[T_DOWN].sc, s.hq, s.hd,
+                     offsets, perm, act, wts, L.d.n_used, T, shared, L.d.n_expert, L.d.hidden, L.d.ffn / 32, s.y);
+}
+
+static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
+                                  int T, float *out, uint32_t flags, hipStream_t st) {
+  const moe_layer_desc &d = L.d;
+  const int k = d.n_used, E = d.n_expert, P = T * k;
+  const bool per_slot = flags & MOE_FWD_PER_SLOT;
+  const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
+  const int KBh = d.hidden / 32, KBf = d.ffn / 32;
+  const int nb_gu = ceil_div(KBh, 64), nb_dn = ceil_div(KBf, 64);
+  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || nb_gu > 6 || nb_dn > 2 || d.hidden % 8)
+    return fail(c, MOE_ERR_UNSUPPORTED, "grouped: shape outside kernel range");
+  scratch &s = c->sc;
+  int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *act = inv + P;
+  hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div((long)T * KBh, 256)), dim3(256), 0, st, x, (uint32_t)(T * KBh),
+                     s.xq, s.xd, (int8_t *)nullptr, (uint16_t *)nullptr);
+  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, ids, P, E, counts, offsets, perm, inv, act);
+  const int ny = (P < E ? P : E) + shared;
+  const dim3 ggu(d.ffn / 32, ny);
+  switch (nb_gu) {
+    case 1: launch_gu_grouped<1>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+    case 2: launch_gu_grouped<2>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+    case 3: launch_gu_grouped<3>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+    case 4: launch_gu_grouped<4>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+    case 5: launch_gu_grouped<5>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+    default: launch_gu_grouped<6>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+  }
+  s.h_rows = (size_t)P + (shared ? T : 0);
+  s.last_F = d.ffn;
+  const dim3 gdn(d.hidden / 8, ny);
+  if (nb_dn == 1) launch_down_grouped<1, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
+  else launch_down_grouped<2, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
+  hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * d.hidden, 256)), dim3(256), 0, st, s.y, inv, T, k,
+                     d.hidden, shared, per_slot ? 1 : 0, out);
+  HIPC(c, hipGetLastError());
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_forward(moe_ctx *c, int layer, const float *x, const int32_t *ids, const float *wts,
+                                  int T, float *out, uint32_t flags, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (c->inject & 1) return fail(c, MOE_ERR_INJECTED, "forward failure injected by MOE_BLOCK_INJECT");
+  if (!x || !ids || !wts || !out || T <= 0) return fail(c, MOE_ERR_INVALID_ARG, "moe_forward: bad arguments");
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident; CPU fallback", layer);
+  dev_layer &L = it->second;
+  if (!c->capturing) HIPC(c, hipSetDevice(c->device));
+  moe_status st = scratch_reserve(c, T, L.d.hidden, L.d.ffn, L.d.n_expert, L.d.n_used);
+  if (st != MOE_OK) return st;
+  if (T == 1) return forward_decode(c, L, x, ids, wts, out, flags, (hipStream_t)stream);
+  return forward_grouped(c, L, x, ids, wts, T, out, flags, (hipStream_t)stream);
+}
+
+extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, const int32_t *ids,
+                                       const float *wts, int T, float *out, uint32_t flags) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!x || !ids || !wts || !out || T <= 0) return fail(c, MOE_ERR_INVALID_ARG, "moe_forward_host: bad arguments");
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident; CPU fallback", layer);
+  const moe_layer_desc &d = it->second.d;
+  HIPC(c, hipSetDevice(c->device));
+  moe_status st = scratch_reserve(c, T, d.hidden, d.ffn, d.n_expert, d.n_used);
+  if (st != MOE_OK) return st;
+  scratch &s = c->sc;
+  const size_t P = (size_t)T * d.n_used;
+  const size_t n_out = (flags & MOE_FWD_PER_SLOT) ? P * d.hidden : (size_t)T * d.hidden;
+  HIPC(c, hipMemcpy(s.x_in, x, (size_t)T * d.hidden * 4, hipMemcpyHostToDevice));
+  HIPC(c, hipMemcpy(s.ids_in, ids, P * 4, hipMemcpyHostToDevice));
+  HIPC(c, hipMemcpy(s.wts_in, wts, P * 4, hipMemcpyHostToDevice));
+  st = moe_forward(c, layer, s.x_in, s.ids_in, s.wts_in, T, s.out_buf, flags, nullptr);
+  if (st != MOE_OK) return st;
+  HIPC(c, hipMemcpy(out, s.out_buf, n_out * 4, hipMemcpyDeviceToHost));
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_route_forward(moe_ctx *c, int layer, const float *x, const float *logits,
+                                        const float *bias, int T, int mode, int norm, float scale, int32_t *ids,
+                                        float *wts, float *out, uint32_t flags, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident; CPU fallback", layer);
+  const moe_layer_desc &d = it->second.d;
+  moe_status st = moe_route(c, logits, bias, T, d.n_expert, d.n_used, mode, norm, scale, ids, wts, stream);
+  if (st != MOE_OK) return st;
+  return moe_forward(c, layer, x, ids, wts, T, out, flags, stream);
+}
+
+// ---------------------------------------------------------------------------
+// graphs
+
+extern "C" moe_status moe_graph_capture(moe_ctx *c, int n_layers, const int *layers, const float *const *x,
+                                        const int32_t *const *ids, const float *const *wts, float *const *out,
+                                        int T, uint32_t flags, moe_graph **g) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!g || n_layers <= 0 || !layers || !x || !ids || !wts || !out || T <= 0)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_graph_capture: bad arguments");
+  *g = nullptr;
+  for (int i = 0; i < n_layers; i++) {
+    auto it = c->layers.find(layers[i]);
+    if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layers[i]);
+    const moe_layer_desc &d = it->second.d;
+    const scratch &s = c->sc;
+    if (!s.xq || T > s.T || d.hidden > s.H || d.ffn > s.F || d.n_expert > s.E || d.n_used > s.k)
+      return fail(c, MOE_ERR_INVALID_ARG, "moe_graph_capture: call moe_ctx_reserve for this shape first");
+  }
+  HIPC(c, hipSetDevice(c->device));
+  HIPC(c, hipDeviceSynchronize());
+  hipStream_t st;
+  HIPC(c, hipStreamCreateWithFlags(&st, hipStreamNonBlocking));
+  moe_status res = MOE_OK;
+  if (hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal) != hipSuccess) {
+    (void)hipStreamDestroy(st);
+    return fail(c, MOE_ERR_HIP, "hipStreamBeginCapture failed");
+  }
+  c->capturing = true;
+  for (int i = 0; i < n_layers && res == MOE_OK; i++)
+    res = moe_forward(c, layers[i], x[i], ids[i], wts[i], T, out[i], flags, st);
+  c->capturing = false;
+  hipGraph_t graph = nullptr;
+  hipError_t e = hipStreamEndCapture(st, &graph);
+  (void)hipStreamDestroy(st);
+  if (res != MOE_OK) {
+    if (graph) (void)hipGraphDestroy(graph);
+    return res;
+  }
+  if (e != hipSuccess || !graph) return fail(c, MOE_ERR_HIP, "hipStreamEndCapture failed");
+  hipGraphExec_t exec = nullptr;
+  if (hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0) != hipSuccess) {
+    (void)hipGraphDestroy(graph);
+    return fail(c, MOE_ERR_HIP, "hipGraphInstantiate failed");
+  }
+  moe_graph *mg = new moe_graph;
+  mg->ctx = c;
+  mg->graph = graph;
+  mg->exec = exec;
+  *g = mg;
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_graph_launch(moe_graph *g, void *stream) {
+  if (!g) return MOE_ERR_INVALID_ARG;
+  HIPC(g->ctx, hipGraphLaunch(g->exec, (hipStream_t)stream));
+  return MOE_OK;
+}
+
+extern "C" void moe_graph_destroy(moe_graph *g) {
+  if (!g) return;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
+}
+
+// ---------------------------------------------------------------------------
+// test hooks
+
+extern "C" moe_status moe_debug_quantize_q8_0(moe_ctx *c, const float *x, int n, int8_t *qs, uint16_t *d,
+                                              void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!x || !qs || !d || n <= 0 || n % 32) return fail(c, MOE_ERR_INVALID_ARG, "moe_debug_quantize_q8_0: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  const int nb = n / 32;
+  uint32_t *tq = nullptr;
+  float *td = nullptr;
+  HIPC(c, hipMalloc(&tq, (size_t)nb * 64));
+  HIPC(c, hipMalloc(&td, (size_t)nb * 4));
+  hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div(nb, 256)), dim3(256), 0, (hipStream_t)stream, x, (uint32_t)nb,
+                     tq, td, qs, d);
+  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
+  (void)hipFree(tq);
+  (void)hipFree(td);
+  if (e != hipSuccess) return fail(c, MOE_ERR_HIP, "moe_debug_quantize_q8_0 failed");
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_debug_wave_sum(moe_ctx *c, const float *x, int n_waves, float *out, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!x || !out || n_waves <= 0) return fail(c, MOE_ERR_INVALID_ARG, "moe_debug_wave_sum: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  hipLaunchKernelGGL(k_debug_wave_sum, dim3(n_waves), dim3(64), 0, (hipStream_t)stream, x, out);
+  HIPC(c, hipGetLastError());
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_debug_last_h(moe_ctx *c, float *h, size_t cap, size_t *n) {
+  if (!c || !h || !n) return MOE_ERR_INVALID_ARG;
+  const size_t rows = c->sc.h_rows, F = (size_t)c->sc.last_F;
+  const size_t cnt = rows * F < cap ? rows * F : cap;
+  HIPC(c, hipDeviceSynchronize());
+  if (cnt) HIPC(c, hipMemcpy(h, c->sc.htap, cnt * 4, hipMemcpyDeviceToHost));
+  *n = cnt;
+  return MOE_OK;
+}

@@ -1,0 +1,296 @@
+"""Python binding of the gfx950 MoE block (ctypes over libmoe_block.so).
+
+A thin host-side mirror of the C-ABI in include/moe_block.h.  Device
+buffers are torch tensors on a ROCm device (torch is only the allocator and
+stream owner here); every computation runs in the HIP library.  There is no
+CPU fallback in this module: if the library is missing or a call fails, a
+MoeError is raised and the caller decides (the reference's backend falls
+back to ggml-cpu at that point, moe-serv/src/moe_backend.cpp:436-445).
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libmoe_block.so")
+
+MOE_OK = 0
+MOE_ERR_INVALID_ARG = -1
+MOE_ERR_HIP = -2
+MOE_ERR_OUT_OF_BUDGET = -3
+MOE_ERR_UNSUPPORTED = -4
+MOE_ERR_NOT_RESIDENT = -5
+MOE_ERR_NO_DEVICE = -6
+MOE_ERR_INJECTED = -7
+
+MOE_FWD_PER_SLOT = 1
+MOE_FWD_NO_SHARED = 2
+
+ROUTE_SOFTMAX, ROUTE_SIGMOID, ROUTE_SQRT_SOFTPLUS = 0, 1, 2
+T_GATE, T_UP, T_DOWN = 0, 1, 2
+
+# every entry point include/moe_block.h declares
+EXPORTS = (
+    "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_last_error", "moe_status_str", "moe_ctx_budget_left",
+    "moe_ctx_reserve", "moe_layer_upload", "moe_layer_generate", "moe_layer_read_blocks",
+    "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward", "moe_forward_host",
+    "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
+    "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
+)
+
+
+class MoeError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        super().__init__(f"{message} (status {status})")
+        self.status = status
+
+
+class LayerDesc(ctypes.Structure):
+    _fields_ = [("hidden", ctypes.c_int32), ("ffn", ctypes.c_int32), ("n_expert", ctypes.c_int32),
+                ("n_used", ctypes.c_int32), ("has_shared", ctypes.c_int32), ("clamp", ctypes.c_float)]
+
+    @classmethod
+    def of(cls, shape) -> "LayerDesc":
+        return cls(shape.hidden, shape.ffn, shape.n_expert, shape.n_used, int(shape.has_shared),
+                   float(shape.clamp))
+
+
+_vp = ctypes.c_void_p
+_lib = None
+
+
+def load_library(path: str | None = None):
+    """Load libmoe_block.so; raises MoeError if it has not been built."""
+    global _lib
+    if _lib is not None and path is None:
+        return _lib
+    p = path or LIB_PATH
+    if not os.path.exists(p):
+        raise MoeError(MOE_ERR_NO_DEVICE, f"{p} is not built (run __graft_entry__.build())")
+    L = ctypes.CDLL(p)
+    st = ctypes.c_int
+    L.moe_ctx_create.restype = st
+    L.moe_ctx_create.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(_vp)]
+    L.moe_ctx_destroy.restype = None
+    L.moe_ctx_destroy.argtypes = [_vp]
+    L.moe_ctx_last_error.restype = ctypes.c_char_p
+    L.moe_ctx_last_error.argtypes = [_vp]
+    L.moe_status_str.restype = ctypes.c_char_p
+    L.moe_status_str.argtypes = [st]
+    L.moe_ctx_budget_left.restype = ctypes.c_uint64
+    L.moe_ctx_budget_left.argtypes = [_vp]
+    L.moe_ctx_reserve.restype = st
+    L.moe_ctx_reserve.argtypes = [_vp, ctypes.POINTER(LayerDesc), ctypes.c_int]
+    L.moe_layer_upload.restype = st
+    L.moe_layer_upload.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(LayerDesc)] + [_vp] * 6
+    L.moe_layer_generate.restype = st
+    L.moe_layer_generate.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(LayerDesc), ctypes.c_uint64,
+                                     ctypes.c_int, ctypes.c_int]
+    L.moe_layer_read_blocks.restype = st
+    L.moe_layer_read_blocks.argtypes = [_vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp]
+    L.moe_layer_release.restype = st
+    L.moe_layer_release.argtypes = [_vp, ctypes.c_int]
+    L.moe_layer_bytes.restype = st
+    L.moe_layer_bytes.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(ctypes.c_uint64)]
+    L.moe_route.restype = st
+    L.moe_route.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                            ctypes.c_int, ctypes.c_float, _vp, _vp, _vp]
+    L.moe_group.restype = st
+    L.moe_group.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
+    L.moe_forward.restype = st
+    L.moe_forward.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, _vp, ctypes.c_uint32, _vp]
+    L.moe_forward_host.restype = st
+    L.moe_forward_host.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, _vp, ctypes.c_uint32]
+    L.moe_route_forward.restype = st
+    L.moe_route_forward.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, ctypes.c_int,
+                                    ctypes.c_int, ctypes.c_float, _vp, _vp, _vp, ctypes.c_uint32, _vp]
+    L.moe_graph_capture.restype = st
+    L.moe_graph_capture.argtypes = [_vp, ctypes.c_int, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_vp),
+                                    ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                                    ctypes.c_int, ctypes.c_uint32, ctypes.POINTER(_vp)]
+    L.moe_graph_launch.restype = st
+    L.moe_graph_launch.argtypes = [_vp, _vp]
+    L.moe_graph_destroy.restype = None
+    L.moe_graph_destroy.argtypes = [_vp]
+    L.moe_debug_quantize_q8_0.restype = st
+    L.moe_debug_quantize_q8_0.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp, _vp]
+    L.moe_debug_wave_sum.restype = st
+    L.moe_debug_wave_sum.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp]
+    L.moe_debug_last_h.restype = st
+    L.moe_debug_last_h.argtypes = [_vp, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    if path is None:
+        _lib = L
+    return L
+
+
+def _ptr(t) -> int | None:
+    """Device pointer of a torch tensor (or None)."""
+    return None if t is None else int(t.data_ptr())
+
+
+def _stream(stream) -> int | None:
+    if stream is None:
+        import torch
+        return int(torch.cuda.current_stream().cuda_stream)
+    return int(stream)
+
+
+class Graph:
+    def __init__(self, ctx: "MoeBlock", handle: int, keep):
+        self._ctx, self._h, self._keep = ctx, handle, keep
+
+    def launch(self, stream=None):
+        self._ctx._check(self._ctx.lib.moe_graph_launch(self._h, _stream(stream)), "moe_graph_launch")
+
+    def close(self):
+        if self._h:
+            self._ctx.lib.moe_graph_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+class MoeBlock:
+    """One device context: resident layers plus per-call scratch."""
+
+    def __init__(self, device: int = 0, budget_bytes: int = 2 ** 64 - 1, lib_path: str | None = None):
+        self.lib = load_library(lib_path)
+        h = _vp()
+        st = self.lib.moe_ctx_create(device, budget_bytes, ctypes.byref(h))
+        if st != MOE_OK:
+            raise MoeError(st, f"moe_ctx_create: {self.lib.moe_status_str(st).decode()}")
+        self.h = h.value
+        self.descs: dict[int, LayerDesc] = {}
+
+    # -- lifecycle --------------------------------------------------------
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.moe_ctx_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int, what: str):
+        if st != MOE_OK:
+            msg = self.lib.moe_ctx_last_error(self.h).decode() if self.h else ""
+            raise MoeError(st, f"{what}: {self.lib.moe_status_str(st).decode()}: {msg}")
+
+    @property
+    def budget_left(self) -> int:
+        return int(self.lib.moe_ctx_budget_left(self.h))
+
+    def reserve(self, shape, max_tokens: int):
+        d = LayerDesc.of(shape)
+        self._check(self.lib.moe_ctx_reserve(self.h, ctypes.byref(d), max_tokens), "moe_ctx_reserve")
+
+    # -- residency ----------------------------------------------------------
+    def upload_layer(self, layer: int, shape, gate: np.ndarray, up: np.ndarray, down: np.ndarray,
+                     shared=None):
+        d = LayerDesc.of(shape)
+        arrs = [np.ascontiguousarray(a, np.uint8) for a in (gate, up, down)]
+        sh = [np.ascontiguousarray(a, np.uint8) for a in shared] if shared is not None else [None] * 3
+        ptrs = [a.ctypes.data if a is not None else None for a in arrs + sh]
+        self._check(self.lib.moe_layer_upload(self.h, layer, ctypes.byref(d), *ptrs), "moe_layer_upload")
+        self.descs[layer] = d
+
+    def generate_layer(self, layer: int, shape, seed: int, e_lo: int = 124, e_span: int = 7):
+        d = LayerDesc.of(shape)
+        self._check(self.lib.moe_layer_generate(self.h, layer, ctypes.byref(d), seed, e_lo, e_span),
+                    "moe_layer_generate")
+        self.descs[layer] = d
+
+    def read_blocks(self, layer: int, tensor: int, expert: int) -> np.ndarray:
+        d = self.descs[layer]
+        rows, K = (d.ffn, d.hidden) if tensor in (T_GATE, T_UP) else (d.hidden, d.ffn)
+        out = np.empty((rows, K // 32, 17), np.uint8)
+        self._check(self.lib.moe_layer_read_blocks(self.h, layer, tensor, expert, out.ctypes.data),
+                    "moe_layer_read_blocks")
+        return out
+
+    def release_layer(self, layer: int):
+        self._check(self.lib.moe_layer_release(self.h, layer), "moe_layer_release")
+        self.descs.pop(layer, None)
+
+    def layer_bytes(self, layer: int) -> int:
+        v = ctypes.c_uint64()
+        self._check(self.lib.moe_layer_bytes(self.h, layer, ctypes.byref(v)), "moe_layer_bytes")
+        return int(v.value)
+
+    # -- per call (torch device tensors) ---------------------------------------
+    def route(self, logits, k: int, mode: int, norm: bool, scale: float, ids, wts, bias=None, stream=None):
+        T, E = logits.shape
+        self._check(self.lib.moe_route(self.h, _ptr(logits), _ptr(bias), T, E, k, mode, int(norm), scale,
+                                       _ptr(ids), _ptr(wts), _stream(stream)), "moe_route")
+
+    def group(self, ids, E: int, counts, offsets, perm, inv=None, stream=None):
+        T, k = ids.shape
+        self._check(self.lib.moe_group(self.h, _ptr(ids), T, k, E, _ptr(counts), _ptr(offsets), _ptr(perm),
+                                       _ptr(inv), _stream(stream)), "moe_group")
+
+    def forward(self, layer: int, x, ids, wts, out, flags: int = 0, stream=None):
+        T = x.shape[0]
+        self._check(self.lib.moe_forward(self.h, layer, _ptr(x), _ptr(ids), _ptr(wts), T, _ptr(out), flags,
+                                         _stream(stream)), "moe_forward")
+
+    def route_forward(self, layer: int, x, logits, ids, wts, out, mode: int, norm: bool = True,
+                      scale: float = 1.0, bias=None, flags: int = 0, stream=None):
+        T = x.shape[0]
+        self._check(self.lib.moe_route_forward(self.h, layer, _ptr(x), _ptr(logits), _ptr(bias), T, mode,
+                                               int(norm), scale, _ptr(ids), _ptr(wts), _ptr(out), flags,
+                                               _stream(stream)), "moe_route_forward")
+
+    def forward_host(self, layer: int, x: np.ndarray, ids: np.ndarray, wts: np.ndarray,
+                     flags: int = 0) -> np.ndarray:
+        d = self.descs[layer]
+        x = np.ascontiguousarray(x, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        wts = np.ascontiguousarray(wts, np.float32)
+        T = x.shape[0]
+        shape = (T, d.n_used, d.hidden) if flags & MOE_FWD_PER_SLOT else (T, d.hidden)
+        out = np.empty(shape, np.float32)
+        self._check(self.lib.moe_forward_host(self.h, layer, x.ctypes.data, ids.ctypes.data, wts.ctypes.data,
+                                              T, out.ctypes.data, flags), "moe_forward_host")
+        return out
+
+    def graph_capture(self, layers, xs, ids, wts, outs, flags: int = 0) -> Graph:
+        n = len(layers)
+        T = xs[0].shape[0]
+        la = (ctypes.c_int * n)(*layers)
+        mk = lambda ts: (_vp * n)(*[_ptr(t) for t in ts])  # noqa: E731
+        px, pi, pw, po = mk(xs), mk(ids), mk(wts), mk(outs)
+        g = _vp()
+        self._check(self.lib.moe_graph_capture(self.h, n, la, px, pi, pw, po, T, flags, ctypes.byref(g)),
+                    "moe_graph_capture")
+        return Graph(self, g.value, (xs, ids, wts, outs))
+
+    # -- test hooks -------------------------------------------------------------
+    def debug_quantize_q8_0(self, x, qs, d, stream=None):
+        self._check(self.lib.moe_debug_quantize_q8_0(self.h, _ptr(x), x.numel(), _ptr(qs), _ptr(d),
+                                                     _stream(stream)), "moe_debug_quantize_q8_0")
+
+    def debug_wave_sum(self, x, out, stream=None):
+        self._check(self.lib.moe_debug_wave_sum(self.h, _ptr(x), x.numel() // 64, _ptr(out), _stream(stream)),
+                    "moe_debug_wave_sum")
+
+    def debug_last_h(self, cap: int) -> np.ndarray:
+        buf = np.empty(cap, np.float32)
+        n = ctypes.c_size_t()
+        self._check(self.lib.moe_debug_last_h(self.h, buf.ctypes.data, cap, ctypes.byref(n)), "moe_debug_last_h")
+        return buf[: n.value]

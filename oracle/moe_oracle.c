@@ -1,0 +1,461 @@
+/*
+ * moe_oracle.c -- CPU restatement of the reference's MoE-block oracle path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the checker and the CPU-baseline leg); the HIP
+ * product never links or calls this file.  See moe_oracle.h for the scope.
+ *
+ * Build: oracle/Makefile (gcc -O2 -ffp-contract=off, so every f32 operation
+ * below rounds exactly where it is written).
+ */
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ------------------------------------------------------------------------ */
+/* number formats                                                           */
+/* ------------------------------------------------------------------------ */
+
+/* Doubled e2m1 values; index 8 is -0 == 0 (hip-moe/src/main.hip:49-50). */
+const int8_t mo_kvalues[16] = {0, 1, 2, 3, 4, 6, 8, 12,
+                               0, -1, -2, -3, -4, -6, -8, -12};
+
+static inline float bits_to_f32(uint32_t u) {
+  float f;
+  memcpy(&f, &u, 4);
+  return f;
+}
+static inline uint32_t f32_to_bits(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  return u;
+}
+
+/* hip-moe/src/main.hip:52-57: half of the E8M0 scale, i.e. 2^(e-128); the
+ * e<2 patterns are f32 denormals. */
+float mo_e8m0_half(uint8_t e) {
+  const uint32_t bits = e < 2 ? (0x00200000u << e) : ((uint32_t)(e - 1) << 23);
+  return bits_to_f32(bits);
+}
+
+/* v >> s rounded to nearest, ties to even (s >= 1). */
+static uint32_t rshift_rne(uint32_t v, int s) {
+  if (s >= 32) return 0; /* v < 2^24 here, so v / 2^s < 1/2 */
+  const uint32_t q = v >> s;
+  const uint32_t rem = v & ((1u << s) - 1u);
+  const uint32_t half = 1u << (s - 1);
+  return q + ((rem > half || (rem == half && (q & 1u))) ? 1u : 0u);
+}
+
+/* IEEE binary32 -> binary16, round-to-nearest-even, overflow to inf.  This
+ * is what F16C's _cvtss_sh(x, 0), i.e. ggml's GGML_CPU_FP32_TO_FP16 on x86,
+ * computes. */
+uint16_t mo_fp32_to_fp16(float f) {
+  const uint32_t x = f32_to_bits(f);
+  const uint16_t sign = (uint16_t)((x >> 16) & 0x8000u);
+  const uint32_t exp = (x >> 23) & 0xffu;
+  const uint32_t man = x & 0x7fffffu;
+  if (exp == 0xffu) return (uint16_t)(sign | 0x7c00u | (man ? 0x200u | (man >> 13) : 0u));
+  if (exp == 0u) return sign; /* f32 zero/denormal: far below fp16 range */
+  const int e16 = (int)exp - 127 + 15;
+  if (e16 >= 1) {
+    const uint32_t h = ((uint32_t)e16 << 10) + rshift_rne(man, 13); /* carry ok */
+    return (uint16_t)(sign | (h >= 0x7c00u ? 0x7c00u : h));
+  }
+  /* fp16 subnormal range: value = (man|2^23) * 2^(exp-150) = m * 2^-24 */
+  return (uint16_t)(sign | rshift_rne(man | 0x800000u, 126 - (int)exp));
+}
+
+float mo_fp16_to_fp32(uint16_t h) {
+  const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+  const uint32_t exp = ((uint32_t)h >> 10) & 0x1fu;
+  const uint32_t man = (uint32_t)h & 0x3ffu;
+  if (exp == 0x1fu) return bits_to_f32(sign | 0x7f800000u | (man << 13));
+  if (exp == 0u) {
+    /* subnormal: man * 2^-24, exact in f32 */
+    const float v = (float)man * 5.9604644775390625e-08f;
+    return sign ? -v : v;
+  }
+  return bits_to_f32(sign | ((exp + 112u) << 23) | (man << 13));
+}
+
+uint16_t mo_fp32_to_bf16(float f) {
+  const uint32_t x = f32_to_bits(f);
+  if ((x & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((x >> 16) | 0x40u); /* NaN */
+  return (uint16_t)((x + 0x7fffu + ((x >> 16) & 1u)) >> 16);
+}
+
+float mo_bf16_to_fp32(uint16_t b) { return bits_to_f32((uint32_t)b << 16); }
+
+/* hip-moe/src/main.hip:82-95: element j of a block is qs[j] & 0xF, element
+ * j+16 is qs[j] >> 4; value = kvalue * e8m0_half(e). */
+void mo_dequant_mxfp4_row(const uint8_t *blocks, int K, float *out) {
+  for (int b = 0; b < K / MO_QK; b++) {
+    const uint8_t *blk = blocks + (size_t)b * MO_MXFP4_BYTES;
+    const float sc = mo_e8m0_half(blk[0]);
+    for (int j = 0; j < 16; j++) {
+      out[b * MO_QK + j] = (float)mo_kvalues[blk[1 + j] & 0x0f] * sc;
+      out[b * MO_QK + j + 16] = (float)mo_kvalues[blk[1 + j] >> 4] * sc;
+    }
+  }
+}
+
+/* ggml quantize_row_q8_0, x86 path (un-vendored; restated):
+ *   amax = max |x| over the block; d = amax / 127 (f32) stored as fp16;
+ *   id = amax != 0 ? 127 / amax : 0; q = round-half-even(x * id).
+ * The scalar reference path instead uses id = 1/d and roundf; the two can
+ * differ by one code on exact ties -- parity unpinned against ggml. */
+void mo_quantize_q8_0(const float *x, int K, int8_t *qs, uint16_t *d) {
+  for (int b = 0; b < K / MO_QK; b++) {
+    const float *xb = x + (size_t)b * MO_QK;
+    float amax = 0.0f;
+    for (int j = 0; j < MO_QK; j++) {
+      const float a = fabsf(xb[j]);
+      amax = a > amax ? a : amax;
+    }
+    const float dd = amax / 127.0f;
+    d[b] = mo_fp32_to_fp16(dd);
+    const float id = amax != 0.0f ? 127.0f / amax : 0.0f;
+    for (int j = 0; j < MO_QK; j++) {
+      /* nearbyintf under the default rounding mode is half-to-even */
+      qs[(size_t)b * MO_QK + j] = (int8_t)(int)nearbyintf(xb[j] * id);
+    }
+  }
+}
+
+int32_t mo_block_isum(const uint8_t *wblock, const int8_t *q) {
+  int32_t lo = 0, hi = 0;
+  for (int j = 0; j < 16; j++) {
+    lo += (int32_t)q[j] * mo_kvalues[wblock[1 + j] & 0x0f];
+    hi += (int32_t)q[j + 16] * mo_kvalues[wblock[1 + j] >> 4];
+  }
+  return lo + hi;
+}
+
+/* ggml_vec_dot_mxfp4_q8_0, generic (scalar) order: per block the exact int
+ * sum, scaled by fp16(d_y) * e8m0_half(e_x), accumulated in f32 in
+ * ascending block order.  ggml's AVX2 body accumulates two blocks per step
+ * in 8 lanes then sums horizontally: the per-block terms are identical, only
+ * the f32 summation order differs (parity unpinned at that level). */
+float mo_vec_dot_mxfp4_q8_0(int K, const uint8_t *wrow, const int8_t *qs,
+                            const uint16_t *d) {
+  float acc = 0.0f;
+  for (int b = 0; b < K / MO_QK; b++) {
+    const uint8_t *blk = wrow + (size_t)b * MO_MXFP4_BYTES;
+    const float s = mo_fp16_to_fp32(d[b]) * mo_e8m0_half(blk[0]);
+    acc += s * (float)mo_block_isum(blk, qs + (size_t)b * MO_QK);
+  }
+  return acc;
+}
+
+/* ------------------------------------------------------------------------ */
+/* routing                                                                  */
+/* ------------------------------------------------------------------------ */
+
+/* softplus as ggml states it: x for x > 20, else log1p(exp(x)). */
+static float softplus_f32(float x) { return x > 20.0f ? x : log1pf(expf(x)); }
+
+void mo_route_scores(const float *logits, int T, int E, int mode, float *probs) {
+  for (int t = 0; t < T; t++) {
+    const float *l = logits + (size_t)t * E;
+    float *p = probs + (size_t)t * E;
+    if (mode == MO_ROUTE_SOFTMAX) {
+      /* ggml soft_max: exp(l - max), sum in double, scale by (float)(1/sum) */
+      float mx = -INFINITY;
+      for (int e = 0; e < E; e++) mx = l[e] > mx ? l[e] : mx;
+      double sum = 0.0;
+      for (int e = 0; e < E; e++) {
+        p[e] = expf(l[e] - mx);
+        sum += (double)p[e];
+      }
+      const float inv = (float)(1.0 / sum);
+      for (int e = 0; e < E; e++) p[e] *= inv;
+    } else if (mode == MO_ROUTE_SIGMOID) {
+      for (int e = 0; e < E; e++) p[e] = 1.0f / (1.0f + expf(-l[e]));
+    } else {
+      for (int e = 0; e < E; e++) p[e] = sqrtf(softplus_f32(l[e]));
+    }
+  }
+}
+
+void mo_route(const float *logits, const float *bias, int T, int E, int k,
+              int mode, int norm, float scale, int32_t *ids, float *wts) {
+  float *probs = (float *)malloc(sizeof(float) * (size_t)E);
+  float *sel = (float *)malloc(sizeof(float) * (size_t)E);
+  unsigned char *taken = (unsigned char *)malloc((size_t)E);
+  for (int t = 0; t < T; t++) {
+    mo_route_scores(logits + (size_t)t * E, 1, E, mode, probs);
+    for (int e = 0; e < E; e++) sel[e] = bias ? probs[e] + bias[e] : probs[e];
+    memset(taken, 0, (size_t)E);
+    for (int s = 0; s < k; s++) {
+      int best = -1;
+      for (int e = 0; e < E; e++) {
+        if (taken[e]) continue;
+        if (best < 0 || sel[e] > sel[best]) best = e; /* strict: lower index wins ties */
+      }
+      taken[best] = 1;
+      ids[(size_t)t * k + s] = best;
+      wts[(size_t)t * k + s] = probs[best]; /* weights from the unbiased scores */
+    }
+    float *w = wts + (size_t)t * k;
+    if (norm) {
+      double sum = 0.0; /* ggml_sum_rows: double accumulator */
+      for (int s = 0; s < k; s++) sum += (double)w[s];
+      float fs = (float)sum;
+      fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs; /* 2^-14 floor */
+      for (int s = 0; s < k; s++) w[s] = w[s] / fs;
+    }
+    if (scale != 0.0f && scale != 1.0f) {
+      for (int s = 0; s < k; s++) w[s] *= scale;
+    }
+  }
+  free(probs);
+  free(sel);
+  free(taken);
+}
+
+/* ------------------------------------------------------------------------ */
+/* grouping                                                                 */
+/* ------------------------------------------------------------------------ */
+
+/* The mul_mat_id row map: visit (t, s) token-major, slot-minor and append
+ * the pair to its expert's list (nano-glm/apps/moe-server/main.cpp:413-459
+ * uses the same order). */
+int mo_group(const int32_t *ids, int T, int k, int E, int32_t *counts,
+             int32_t *offsets, int32_t *perm, int32_t *inv) {
+  const int P = T * k;
+  if (E <= 0 || P < 0) return -1;
+  for (int e = 0; e < E; e++) counts[e] = 0;
+  for (int p = 0; p < P; p++) counts[ids[p]]++;
+  int distinct = 0, run = 0;
+  for (int e = 0; e < E; e++) {
+    offsets[e] = run;
+    run += counts[e];
+    distinct += counts[e] > 0;
+  }
+  offsets[E] = run;
+  int32_t *fill = (int32_t *)calloc((size_t)E, sizeof(int32_t));
+  for (int p = 0; p < P; p++) {
+    const int e = ids[p];
+    const int row = offsets[e] + fill[e]++;
+    perm[row] = p;
+    if (inv) inv[p] = row;
+  }
+  free(fill);
+  return distinct;
+}
+
+/* ------------------------------------------------------------------------ */
+/* the block                                                                */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  const mo_layer *L;
+  int T, P, nthreads;
+  const float *x;
+  const int32_t *ids;
+  const float *wts;
+  float *out, *per_slot, *h_routed, *h_shared;
+  /* scratch */
+  int8_t *xq;     /* [T][H]   */
+  uint16_t *xd;   /* [T][H/32] */
+  float *h;       /* [P+T][F] routed pairs then shared rows */
+  int8_t *hq;     /* [P+T][F] */
+  uint16_t *hd;   /* [P+T][F/32] */
+  float *y;       /* [P+T][H] weighted routed rows, then shared rows */
+  pthread_barrier_t bar;
+} fwd_state;
+
+typedef struct {
+  fwd_state *S;
+  int tid;
+} fwd_arg;
+
+static void span(size_t n, int tid, int nt, size_t *b, size_t *e) {
+  *b = n * (size_t)tid / (size_t)nt;
+  *e = n * (size_t)(tid + 1) / (size_t)nt;
+}
+
+static inline float clampf(float v, float lo, float hi) {
+  /* ggml_clamp: MAX(MIN(v, hi), lo) */
+  v = v < hi ? v : hi;
+  return v > lo ? v : lo;
+}
+
+static void *fwd_worker(void *argp) {
+  fwd_arg *a = (fwd_arg *)argp;
+  fwd_state *S = a->S;
+  const mo_layer *L = S->L;
+  const int H = L->H, F = L->F, k = L->k, T = S->T, P = S->P;
+  const int has_sh = L->sh_gate != NULL;
+  const int R = P + (has_sh ? T : 0); /* expert rows: routed pairs, then shared */
+  const size_t gu_row = (size_t)(H / MO_QK) * MO_MXFP4_BYTES;
+  const size_t dn_row = (size_t)(F / MO_QK) * MO_MXFP4_BYTES;
+  size_t b, e;
+
+  /* gate / up / clamp / SwiGLU for every (expert row, ffn column) */
+  span((size_t)R * F, a->tid, S->nthreads, &b, &e);
+  for (size_t i = b; i < e; i++) {
+    const int r = (int)(i / (size_t)F), c = (int)(i % (size_t)F);
+    const uint8_t *gw, *uw;
+    int t;
+    if (r < P) {
+      t = r / k;
+      const int ex = S->ids[r];
+      gw = L->gate[ex] + (size_t)c * gu_row;
+      uw = L->up[ex] + (size_t)c * gu_row;
+    } else {
+      t = r - P;
+      gw = L->sh_gate + (size_t)c * gu_row;
+      uw = L->sh_up + (size_t)c * gu_row;
+    }
+    const int8_t *q = S->xq + (size_t)t * H;
+    const uint16_t *d = S->xd + (size_t)t * (H / MO_QK);
+    float g = mo_vec_dot_mxfp4_q8_0(H, gw, q, d);
+    float u = mo_vec_dot_mxfp4_q8_0(H, uw, q, d);
+    if (L->clamp > 1e-6f) {
+      /* deepseek4 order: up symmetric, gate one-sided, before SiLU */
+      u = clampf(u, -L->clamp, L->clamp);
+      g = clampf(g, -INFINITY, L->clamp);
+    }
+    /* ggml_swiglu_split: silu(gate) * up, silu(x) = x / (1 + exp(-x)) */
+    S->h[(size_t)r * F + c] = (g / (1.0f + expf(-g))) * u;
+  }
+  pthread_barrier_wait(&S->bar);
+
+  /* Q8_0 of every h row (down's src1 conversion) */
+  span((size_t)R, a->tid, S->nthreads, &b, &e);
+  for (size_t r = b; r < e; r++) {
+    mo_quantize_q8_0(S->h + r * F, F, S->hq + r * F, S->hd + r * (F / MO_QK));
+  }
+  pthread_barrier_wait(&S->bar);
+
+  /* down, times the router weight for routed rows (the MUL node) */
+  span((size_t)R * H, a->tid, S->nthreads, &b, &e);
+  for (size_t i = b; i < e; i++) {
+    const int r = (int)(i / (size_t)H), c = (int)(i % (size_t)H);
+    const uint8_t *dw = r < P ? L->down[S->ids[r]] + (size_t)c * dn_row
+                              : L->sh_down + (size_t)c * dn_row;
+    float v = mo_vec_dot_mxfp4_q8_0(F, dw, S->hq + (size_t)r * F,
+                                    S->hd + (size_t)r * (F / MO_QK));
+    if (r < P) v = v * S->wts[r];
+    S->y[(size_t)r * H + c] = v;
+  }
+  pthread_barrier_wait(&S->bar);
+
+  /* pairwise combine in slot order, then + shared (trunk ADDs) */
+  span((size_t)T * H, a->tid, S->nthreads, &b, &e);
+  for (size_t i = b; i < e; i++) {
+    const int t = (int)(i / (size_t)H), c = (int)(i % (size_t)H);
+    float acc = S->y[((size_t)t * k) * H + c];
+    for (int s = 1; s < k; s++) acc = acc + S->y[((size_t)t * k + s) * H + c];
+    if (has_sh) acc = acc + S->y[((size_t)P + t) * H + c];
+    S->out[i] = acc;
+  }
+  return NULL;
+}
+
+int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
+                        const int32_t *ids, const float *wts, float *out,
+                        float *per_slot, float *h_routed, float *h_shared,
+                        int n_threads) {
+  if (!L || T <= 0 || !x || !ids || !wts || !out) return -1;
+  if (L->H % MO_QK || L->F % MO_QK || L->k <= 0 || L->E <= 0) return -1;
+  for (int p = 0; p < T * L->k; p++) {
+    if (ids[p] < 0 || ids[p] >= L->E || !L->gate[ids[p]] || !L->up[ids[p]] ||
+        !L->down[ids[p]])
+      return -1;
+  }
+  const int H = L->H, F = L->F, P = T * L->k;
+  const int R = P + (L->sh_gate ? T : 0);
+  if (n_threads < 1) n_threads = 1;
+
+  fwd_state S;
+  memset(&S, 0, sizeof(S));
+  S.L = L;
+  S.T = T;
+  S.P = P;
+  S.nthreads = n_threads;
+  S.x = x;
+  S.ids = ids;
+  S.wts = wts;
+  S.out = out;
+  S.xq = (int8_t *)malloc((size_t)T * H);
+  S.xd = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * (H / MO_QK));
+  S.h = (float *)malloc(sizeof(float) * (size_t)R * F);
+  S.hq = (int8_t *)malloc((size_t)R * F);
+  S.hd = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)R * (F / MO_QK));
+  S.y = (float *)malloc(sizeof(float) * (size_t)R * H);
+  if (!S.xq || !S.xd || !S.h || !S.hq || !S.hd || !S.y) {
+    free(S.xq); free(S.xd); free(S.h); free(S.hq); free(S.hd); free(S.y);
+    return -1;
+  }
+  /* src1 -> Q8_0, once per token (mul_mat_id broadcasts x over slots) */
+  for (int t = 0; t < T; t++) {
+    mo_quantize_q8_0(x + (size_t)t * H, H, S.xq + (size_t)t * H,
+                     S.xd + (size_t)t * (H / MO_QK));
+  }
+  pthread_barrier_init(&S.bar, NULL, (unsigned)n_threads);
+  pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)n_threads);
+  fwd_arg *args = (fwd_arg *)malloc(sizeof(fwd_arg) * (size_t)n_threads);
+  for (int i = 0; i < n_threads; i++) {
+    args[i].S = &S;
+    args[i].tid = i;
+    if (i) pthread_create(&th[i], NULL, fwd_worker, &args[i]);
+  }
+  fwd_worker(&args[0]);
+  for (int i = 1; i < n_threads; i++) pthread_join(th[i], NULL);
+  pthread_barrier_destroy(&S.bar);
+  free(th);
+  free(args);
+
+  if (per_slot) memcpy(per_slot, S.y, sizeof(float) * (size_t)P * H);
+  if (h_routed) memcpy(h_routed, S.h, sizeof(float) * (size_t)P * F);
+  if (h_shared && L->sh_gate) memcpy(h_shared, S.h + (size_t)P * F, sizeof(float) * (size_t)T * F);
+  free(S.xq); free(S.xd); free(S.h); free(S.hq); free(S.hd); free(S.y);
+  return 0;
+}
+
+int mo_moe_forward(const mo_layer *L, int T, const float *x,
+                   const int32_t *ids, const float *wts, float *out,
+                   float *per_slot, int n_threads) {
+  return mo_moe_forward_taps(L, T, x, ids, wts, out, per_slot, NULL, NULL, n_threads);
+}
+
+/* ------------------------------------------------------------------------ */
+/* synthetic weights                                                        */
+/* ------------------------------------------------------------------------ */
+
+/* SplitMix64's output function applied to state z (Steele, Lea & Flood,
+ * "Fast splittable pseudorandom number generators", OOPSLA 2014). */
+uint64_t mo_mix64(uint64_t z) {
+  z += 0x9e3779b97f4a7c15ull;
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+uint64_t mo_gen_key(uint64_t seed, int layer, int tensor, int expert) {
+  const uint64_t id = ((uint64_t)(uint32_t)layer << 40) ^ ((uint64_t)(uint32_t)tensor << 32) ^
+                      (uint64_t)(uint32_t)expert;
+  return mo_mix64(seed ^ mo_mix64(id));
+}
+
+void mo_gen_mxfp4(uint64_t seed, int layer, int tensor, int expert, int rows,
+                  int K, int e_lo, int e_span, uint8_t *out) {
+  const uint64_t key = mo_gen_key(seed, layer, tensor, expert);
+  const uint64_t nb = (uint64_t)rows * (uint64_t)(K / MO_QK);
+  for (uint64_t i = 0; i < nb; i++) {
+    uint8_t *blk = out + i * MO_MXFP4_BYTES;
+    const uint64_t a = mo_mix64(key + 2 * i + 1);
+    const uint64_t b = mo_mix64(key + 2 * i + 2);
+    const uint64_t c = mo_mix64(key ^ ~i);
+    blk[0] = (uint8_t)(e_lo + (int)(((c >> 32) * (uint64_t)e_span) >> 32));
+    for (int j = 0; j < 8; j++) {
+      blk[1 + j] = (uint8_t)(a >> (8 * j));
+      blk[9 + j] = (uint8_t)(b >> (8 * j));
+    }
+  }
+}

@@ -1,0 +1,266 @@
+"""GPU parity of the whole MoE block against the CPU oracle.
+
+The reference's gates (hip-moe/src/moe_ggml_bench.cpp:308-321: normalise by
+the reference RMS because near-zero outputs make a relative gate meaningless)
+are tightened to the build's contract: max|gpu - oracle| <= 1e-3 * RMS(oracle
+output), expert ids and grouping bit-exact.  Routing is held fixed by feeding
+the oracle's ids/weights to the GPU (the reference's ids_as_input escape
+hatch, moe_ggml_bench.cpp:132-136), and separately checked end to end.
+"""
+import numpy as np
+import pytest
+
+import moe_block as mb
+import workloads as wl
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3  # max-abs error as a fraction of the oracle output's RMS
+
+
+def say(*a):
+    print("[gpu]", *a, flush=True)
+
+
+def rms(a):
+    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
+
+
+def assert_rms_close(got, ref, tol=TOL, what=""):
+    r = rms(ref)
+    err = float(np.max(np.abs(np.asarray(got, np.float64) - ref)))
+    say(f"{what} rms(ref)={r:.4e} max|diff|={err:.3e} ratio={err / r:.3e}")
+    assert err <= tol * r, f"{what}: max|diff| {err:.3e} > {tol} * rms {r:.3e}"
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    return torch, torch.device("cuda:0")
+
+
+@pytest.fixture(scope="module")
+def blk(torch_dev):
+    b = mb.MoeBlock(0)
+    yield b
+    b.close()
+
+
+def run_block(blk, torch_dev, layer, x, ids, wts, flags=0):
+    torch, dev = torch_dev
+    T = x.shape[0]
+    d = blk.descs[layer]
+    shape = (T, d.n_used, d.hidden) if flags & mb.MOE_FWD_PER_SLOT else (T, d.hidden)
+    out = torch.empty(shape, dtype=torch.float32, device=dev)
+    blk.forward(layer, torch.from_numpy(x).to(dev), torch.from_numpy(ids).to(dev),
+                torch.from_numpy(wts).to(dev), out, flags)
+    torch.cuda.synchronize()
+    return out.cpu().numpy()
+
+
+def oracle_layer(oracle, shape, seed, layer, ids, clamp=None, e_lo=124, e_span=7):
+    return oracle.OracleLayer.generated(seed, layer, shape.hidden, shape.ffn, shape.n_expert, shape.n_used,
+                                        experts=sorted(set(np.asarray(ids).ravel().tolist())),
+                                        shared=shape.has_shared,
+                                        clamp=shape.clamp if clamp is None else clamp, e_lo=e_lo, e_span=e_span)
+
+
+# ---- C1: small layer, decode ---------------------------------------------------------
+
+@pytest.fixture(scope="module")
+def c1(blk):
+    blk.generate_layer(1, wl.C1, seed=101)
+    yield wl.C1
+    blk.release_layer(1)
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_c1_decode(blk, torch_dev, oracle, c1, seed):
+    x, lg = wl.make_inputs(c1, 1, seed)
+    ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    say("C1 decode seed", seed, "ids", ids.tolist())
+    got = run_block(blk, torch_dev, 1, x, ids, wts)
+    ref = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts, taps=True)
+    assert_rms_close(got, ref["out"], what="C1")
+    h = blk.debug_last_h(c1.n_used * c1.ffn).reshape(c1.n_used, c1.ffn)
+    assert_rms_close(h, ref["h"][0], tol=1e-4, what="C1 h")
+
+
+def test_c1_decode_per_slot(blk, torch_dev, oracle, c1):
+    x, lg = wl.make_inputs(c1, 1, 5)
+    ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    say("C1 per-slot")
+    got = run_block(blk, torch_dev, 1, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
+    ref = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts, per_slot=True)["per_slot"]
+    for s in range(c1.n_used):
+        assert_rms_close(got[0, s], ref[0, s], what=f"C1 slot {s}")
+
+
+def test_c1_route_forward_end_to_end(blk, torch_dev, oracle, c1):
+    torch, dev = torch_dev
+    x, lg = wl.make_inputs(c1, 1, 9)
+    say("C1 route+forward")
+    ids = torch.empty((1, c1.n_used), dtype=torch.int32, device=dev)
+    wts = torch.empty((1, c1.n_used), dtype=torch.float32, device=dev)
+    out = torch.empty((1, c1.hidden), dtype=torch.float32, device=dev)
+    blk.route_forward(1, torch.from_numpy(x).to(dev), torch.from_numpy(lg).to(dev), ids, wts, out,
+                      mode=c1.route_mode, norm=True)
+    torch.cuda.synchronize()
+    oi, ow = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), oi)
+    ref = oracle_layer(oracle, c1, 101, 1, oi).forward(x, oi, ow)["out"]
+    assert_rms_close(out.cpu().numpy(), ref, what="C1 e2e")
+
+
+def test_c1_forward_host_boundary(blk, oracle, c1):
+    x, lg = wl.make_inputs(c1, 1, 13)
+    ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    say("C1 forward_host")
+    got = blk.forward_host(1, x, ids, wts)
+    ref = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts)["out"]
+    assert_rms_close(got, ref, what="C1 host")
+
+
+def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
+    x, lg = wl.make_inputs(c1, 6, 21, zipf=True)
+    ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    say("C1 grouped T=6", ids.tolist())
+    got = run_block(blk, torch_dev, 1, x, ids, wts)
+    ref = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts)["out"]
+    for t in range(6):
+        assert_rms_close(got[t], ref[t], what=f"C1 grouped t{t}")
+    ps = run_block(blk, torch_dev, 1, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
+    refps = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts, per_slot=True)["per_slot"]
+    assert_rms_close(ps, refps, what="C1 grouped per-slot")
+
+
+# ---- clamp-active (the reference's synthetic weights never trigger the clamp) ---------
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_clamp_active(blk, torch_dev, oracle, T):
+    shape = wl.LayerShape(hidden=1024, ffn=512, n_expert=16, n_used=4, has_shared=True,
+                          route_mode=wl.ROUTE_SIGMOID, clamp=0.75)
+    say("clamp-active T", T)
+    blk.generate_layer(7, shape, seed=55, e_lo=128, e_span=3)
+    try:
+        x, lg = wl.make_inputs(shape, T, 31)
+        ids, wts = oracle.route(lg, shape.n_used, shape.route_mode, norm=True)
+        got = run_block(blk, torch_dev, 7, x, ids, wts)
+        L = oracle_layer(oracle, shape, 55, 7, ids, e_lo=128, e_span=3)
+        ref = L.forward(x, ids, wts, taps=True)
+        unclamped = oracle_layer(oracle, shape, 55, 7, ids, clamp=0.0, e_lo=128, e_span=3).forward(
+            x, ids, wts, taps=True)
+        assert np.abs(unclamped["h"]).max() > 4 * np.abs(ref["h"]).max()  # the clamp binds
+        assert_rms_close(got, ref["out"], what="clamp")
+    finally:
+        blk.release_layer(7)
+
+
+# ---- C2: DeepSeek-V3-shaped layer, decode ------------------------------------------------
+
+@pytest.fixture(scope="module")
+def v3(blk):
+    say("generate V3 layer (6 GB)")
+    blk.generate_layer(2, wl.V3, seed=202)
+    yield wl.V3
+    blk.release_layer(2)
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_c2_decode(blk, torch_dev, oracle, v3, seed):
+    x, lg = wl.make_inputs(v3, 1, seed)
+    ids, wts = oracle.route(lg, v3.n_used, v3.route_mode, norm=True)
+    say("C2 decode seed", seed, ids.tolist())
+    got = run_block(blk, torch_dev, 2, x, ids, wts)
+    ref = oracle_layer(oracle, v3, 202, 2, ids).forward(x, ids, wts, n_threads=16)["out"]
+    assert_rms_close(got, ref, what="C2")
+
+
+def test_c2_route_forward_ids_bit_exact(blk, torch_dev, oracle, v3):
+    torch, dev = torch_dev
+    x, lg = wl.make_inputs(v3, 1, 3)
+    say("C2 route+forward")
+    ids = torch.empty((1, 8), dtype=torch.int32, device=dev)
+    wts = torch.empty((1, 8), dtype=torch.float32, device=dev)
+    out = torch.empty((1, v3.hidden), dtype=torch.float32, device=dev)
+    blk.route_forward(2, torch.from_numpy(x).to(dev), torch.from_numpy(lg).to(dev), ids, wts, out,
+                      mode=v3.route_mode, norm=True)
+    torch.cuda.synchronize()
+    oi, ow = oracle.route(lg, 8, v3.route_mode, norm=True)
+    np.testing.assert_array_equal(ids.cpu().numpy(), oi)
+    ref = oracle_layer(oracle, v3, 202, 2, oi).forward(x, oi, ow, n_threads=16)["out"]
+    assert_rms_close(out.cpu().numpy(), ref, what="C2 e2e")
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("T", [4, 16, 64])
+def test_c3_small_batch_zipf(blk, torch_dev, oracle, v3, T):
+    x, lg = wl.make_inputs(v3, T, 40 + T, zipf=True)
+    ids, wts = oracle.route(lg, 8, v3.route_mode, norm=True)
+    g = oracle.group(ids, v3.n_expert)
+    say("C3 T", T, "distinct", g["distinct"], "max/expert", int(g["counts"].max()))
+    got = run_block(blk, torch_dev, 2, x, ids, wts)
+    ref = oracle_layer(oracle, v3, 202, 2, ids).forward(x, ids, wts, n_threads=16)["out"]
+    for t in range(T):
+        assert_rms_close(got[t], ref[t], what=f"C3 T{T} t{t}")
+
+
+def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
+    torch, dev = torch_dev
+    say("graph capture 2 layers")
+    blk.reserve(v3, 1)
+    xs, idl, wl_, outs, eager = [], [], [], [], []
+    for i, (layer, shape) in enumerate(((1, c1), (2, v3))):
+        x, lg = wl.make_inputs(shape, 1, 70 + i)
+        ids, wts = oracle.route(lg, shape.n_used, shape.route_mode, norm=True)
+        xs.append(torch.from_numpy(x).to(dev))
+        idl.append(torch.from_numpy(ids).to(dev))
+        wl_.append(torch.from_numpy(wts).to(dev))
+        outs.append(torch.zeros((1, shape.hidden), dtype=torch.float32, device=dev))
+        eager.append(run_block(blk, torch_dev, layer, x, ids, wts))
+    g = blk.graph_capture([1, 2], xs, idl, wl_, outs)
+    for rep in range(3):
+        for o in outs:
+            o.zero_()
+        g.launch()
+        torch.cuda.synchronize()
+        for i in range(2):
+            np.testing.assert_array_equal(outs[i].cpu().numpy(), eager[i], err_msg=f"replay {rep} layer {i}")
+        # eager work between replays
+        run_block(blk, torch_dev, 1, xs[0].cpu().numpy(), idl[0].cpu().numpy(), wl_[0].cpu().numpy())
+    g.close()
+
+
+# ---- failure paths, forced from the host ---------------------------------------------------
+
+def test_budget_exhausted_is_reported_not_skipped(torch_dev):
+    say("budget 0")
+    with mb.MoeBlock(0, budget_bytes=0) as b:
+        with pytest.raises(mb.MoeError) as ei:
+            b.generate_layer(0, wl.C1, seed=1)
+        assert ei.value.status == mb.MOE_ERR_OUT_OF_BUDGET
+        assert b.budget_left == 0
+
+
+def test_not_resident_layer_errors(blk, torch_dev):
+    torch, dev = torch_dev
+    say("not resident")
+    x = torch.zeros((1, 2048), device=dev)
+    ids = torch.zeros((1, 4), dtype=torch.int32, device=dev)
+    w = torch.zeros((1, 4), device=dev)
+    out = torch.zeros((1, 2048), device=dev)
+    with pytest.raises(mb.MoeError) as ei:
+        blk.forward(12345, x, ids, w, out)
+    assert ei.value.status == mb.MOE_ERR_NOT_RESIDENT
+
+
+def test_budget_accounting(torch_dev):
+    say("budget accounting")
+    with mb.MoeBlock(0, budget_bytes=wl.C1.layer_bytes + 10) as b:
+        b.generate_layer(0, wl.C1, seed=1)
+        assert b.budget_left == 10
+        with pytest.raises(mb.MoeError):
+            b.generate_layer(1, wl.C1, seed=1)
+        b.release_layer(0)
+        b.generate_layer(1, wl.C1, seed=1)

@@ -1,0 +1,280 @@
+"""Pins the CPU oracle (oracle/moe_oracle.c) before anything is checked against it.
+
+Each check compares the oracle with something it was not derived from: the
+OCP MX format definitions (np_ref.py), numpy's / torch's own float
+conversions, brute force, closed forms and invariants.  The reference ships
+no golden vectors for this path (its gates need llama.cpp + GGUF models), so
+these, plus the committed fixtures in tests/golden/, are what pin it.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import np_ref
+
+
+# ---- number formats ------------------------------------------------------------
+
+def test_e8m0_half_closed_form(oracle):
+    # ggml's e8m0 "half" is 2^(e-128) for every byte, e<2 included (f32 denormals)
+    for e in range(256):
+        assert oracle.e8m0_half(e) == math.ldexp(1.0, e - 128), e
+
+
+def test_dequant_matches_ocp_e2m1_definition(oracle):
+    rng = np.random.default_rng(0)
+    blocks = rng.integers(0, 256, size=(5, 4, 17), dtype=np.uint8)
+    blocks[:, :, 0] = rng.integers(100, 150, size=(5, 4))
+    got = oracle.dequant_mxfp4(blocks, 128).astype(np.float64)
+    np.testing.assert_array_equal(got, np_ref.dequant_blocks(blocks))
+
+
+def test_dequant_element_order(oracle):
+    # byte j: low nibble -> element j, high nibble -> element j+16
+    blk = np.zeros((1, 1, 17), np.uint8)
+    blk[0, 0, 0] = 128  # scale 2^1
+    for j in range(16):
+        blk[0, 0, 1 + j] = (j & 0xF) | (((15 - j) & 0xF) << 4)
+    v = oracle.dequant_mxfp4(blk, 32)[0]
+    for j in range(16):
+        assert v[j] == np_ref.e2m1_value(j) * 2.0
+        assert v[j + 16] == np_ref.e2m1_value(15 - j) * 2.0
+
+
+def test_fp16_conversion_vs_numpy(oracle):
+    rng = np.random.default_rng(1)
+    vals = np.concatenate([
+        rng.standard_normal(2000).astype(np.float32) * np.float32(10.0) ** rng.integers(-9, 6, 2000),
+        np.array([0.0, -0.0, 65504.0, 65519.99, 65520.0, 1e6, -1e6, 6.1e-5, 5.96e-8, 2.98e-8, 2.99e-8,
+                  1.5e-8, np.inf, -np.inf], np.float32),
+    ]).astype(np.float32)
+    for v in vals:
+        want = np.array([v], np.float32).astype(np.float16).view(np.uint16)[0]
+        assert oracle.fp32_to_fp16_bits(float(v)) == want, v
+        back = oracle.fp16_bits_to_fp32(int(want))
+        assert back == float(np.array([want], np.uint16).view(np.float16)[0].astype(np.float32))
+
+
+def test_bf16_conversion_vs_torch(oracle):
+    import torch
+    rng = np.random.default_rng(2)
+    x = rng.standard_normal(5000).astype(np.float32) * 37.0
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = np.array([oracle.lib().mo_fp32_to_bf16(float(v)) for v in x], np.uint16)
+    np.testing.assert_array_equal(got, want)
+
+
+# ---- Q8_0 ------------------------------------------------------------------------
+
+def test_q8_0_invariants(oracle):
+    rng = np.random.default_rng(3)
+    x = (rng.standard_normal((64, 256)) * rng.uniform(1e-3, 50, (64, 1))).astype(np.float32)
+    qs, d = oracle.quantize_q8_0(x)
+    assert np.abs(qs.astype(np.int32)).max() <= 127
+    xb = x.reshape(64, 8, 32).astype(np.float64)
+    qb = qs.reshape(64, 8, 32).astype(np.int32)
+    amax = np.abs(xb).max(axis=2)
+    # every nonzero block reaches +-127 on its largest element
+    assert np.all(np.abs(qb).max(axis=2) == 127)
+    # d is fp16(amax/127)
+    np.testing.assert_array_equal(d, (amax / 127.0).astype(np.float32).astype(np.float16).view(np.uint16))
+    # each code is within half a step of x (step = amax/127, before fp16 rounding of d)
+    step = amax / 127.0
+    assert np.all(np.abs(qb * step[:, :, None] - xb) <= 0.5 * step[:, :, None] * (1 + 1e-5))
+
+
+def test_q8_0_rounds_half_to_even(oracle):
+    # amax = 127 -> id = 1: x * id is exact, so ties are real ties
+    x = np.zeros(32, np.float32)
+    x[0] = 127.0
+    x[1:7] = [2.5, 3.5, -2.5, -3.5, 0.5, -0.5]
+    qs, d = oracle.quantize_q8_0(x)
+    assert qs[1:7].tolist() == [2, 4, -2, -4, 0, 0]  # roundf would give 3, 4, -3, -4, 1, -1
+    assert np.array([d[0]], np.uint16).view(np.float16)[0] == np.float16(1.0)
+
+
+def test_q8_0_zero_block(oracle):
+    qs, d = oracle.quantize_q8_0(np.zeros(64, np.float32))
+    assert not qs.any() and not d.any()
+
+
+# ---- dots ------------------------------------------------------------------------
+
+def test_block_isum_brute_force(oracle):
+    rng = np.random.default_rng(4)
+    kv2 = (np_ref.E2M1 * 2).astype(np.int64)  # doubled e2m1 = ggml's integer kvalues
+    for _ in range(200):
+        blk = rng.integers(0, 256, 17, dtype=np.uint8)
+        q = rng.integers(-127, 128, 32).astype(np.int8)
+        w = np.concatenate([kv2[blk[1:] & 0xF], kv2[blk[1:] >> 4]])
+        assert oracle.block_isum(blk, q) == int(np.dot(w, q.astype(np.int64)))
+
+
+def test_vec_dot_vs_float64(oracle):
+    rng = np.random.default_rng(5)
+    for K in (32, 256, 7168):
+        row = rng.integers(0, 256, (1, K // 32, 17), dtype=np.uint8)
+        row[0, :, 0] = rng.integers(120, 134, K // 32)
+        x = rng.standard_normal(K).astype(np.float32)
+        qs, d = oracle.quantize_q8_0(x)
+        got = oracle.vec_dot(row, qs, d)
+        terms = np_ref.dequant_blocks(row)[0] * np_ref.q8_dequant(qs, d)
+        want = terms.sum()
+        assert abs(got - want) <= 1e-6 * np.abs(terms).sum() + 1e-30, (K, got, want)
+
+
+# ---- routing ---------------------------------------------------------------------
+
+def test_route_sigmoid_closed_form(oracle):
+    rng = np.random.default_rng(6)
+    lg = rng.standard_normal((16, 256)).astype(np.float32)
+    p = oracle.route_scores(lg, oracle.ROUTE_SIGMOID)
+    np.testing.assert_allclose(p, 1.0 / (1.0 + np.exp(-lg.astype(np.float64))), rtol=3e-7)
+    ids, w = oracle.route(lg, 8, oracle.ROUTE_SIGMOID)
+    for t in range(16):
+        assert ids[t].tolist() == np.argsort(-p[t], kind="stable")[:8].tolist()
+        np.testing.assert_allclose(w[t], p[t, ids[t]] / p[t, ids[t]].astype(np.float64).sum(), rtol=1e-6)
+        assert abs(w[t].astype(np.float64).sum() - 1.0) < 1e-6
+
+
+def test_route_softmax_closed_form(oracle):
+    rng = np.random.default_rng(7)
+    lg = rng.standard_normal((16, 32)).astype(np.float32)
+    p = oracle.route_scores(lg, oracle.ROUTE_SOFTMAX)
+    ex = np.exp(lg.astype(np.float64) - lg.max(axis=1, keepdims=True))
+    np.testing.assert_allclose(p, ex / ex.sum(axis=1, keepdims=True), rtol=1e-6)
+    np.testing.assert_allclose(p.sum(axis=1), 1.0, atol=1e-6)
+    ids, w = oracle.route(lg, 4, oracle.ROUTE_SOFTMAX)
+    for t in range(16):
+        assert ids[t].tolist() == np.argsort(-lg[t], kind="stable")[:4].tolist()
+
+
+def test_route_sqrt_softplus_closed_form(oracle):
+    lg = np.linspace(-30, 30, 64, dtype=np.float32)[None, :]
+    p = oracle.route_scores(lg, oracle.ROUTE_SQRT_SOFTPLUS)[0]
+    want = np.sqrt(np.log1p(np.exp(lg[0].astype(np.float64))))
+    np.testing.assert_allclose(p, want, rtol=2e-6)
+
+
+def test_route_bias_selects_but_does_not_weigh(oracle):
+    rng = np.random.default_rng(8)
+    lg = rng.standard_normal((4, 64)).astype(np.float32)
+    bias = np.zeros(64, np.float32)
+    bias[[5, 9, 40]] = 10.0
+    ids, w = oracle.route(lg, 6, oracle.ROUTE_SIGMOID, norm=False, bias=bias)
+    p = oracle.route_scores(lg, oracle.ROUTE_SIGMOID)
+    for t in range(4):
+        assert set(ids[t, :3].tolist()) == {5, 9, 40}
+        np.testing.assert_array_equal(w[t], p[t, ids[t]])
+
+
+def test_route_norm_floor_and_scale(oracle):
+    lg = np.full((1, 8), -40.0, np.float32)  # sigmoid ~ 4e-18: the 2^-14 floor binds
+    lg[0, 3] = -39.0
+    ids, w = oracle.route(lg, 2, oracle.ROUTE_SIGMOID, norm=True, scale=2.5)
+    p = oracle.route_scores(lg, oracle.ROUTE_SIGMOID)[0]
+    assert ids[0].tolist() == [3, 0]  # ties among the rest go to the lower id
+    want = (p[ids[0]] / np.float32(6.103515625e-5)) * np.float32(2.5)
+    np.testing.assert_array_equal(w[0], want.astype(np.float32))
+
+
+def test_route_ties_lower_index_first(oracle):
+    lg = np.zeros((1, 16), np.float32)
+    ids, _ = oracle.route(lg, 5, oracle.ROUTE_SIGMOID)
+    assert ids[0].tolist() == [0, 1, 2, 3, 4]
+
+
+# ---- grouping ---------------------------------------------------------------------
+
+@pytest.mark.parametrize("T,k,E", [(1, 8, 256), (4, 8, 256), (64, 8, 256), (512, 8, 256), (7, 4, 32)])
+def test_group_matches_stable_sort(oracle, T, k, E):
+    rng = np.random.default_rng(T * 1000 + k)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    g = oracle.group(ids, E)
+    flat = ids.ravel()
+    np.testing.assert_array_equal(g["counts"], np.bincount(flat, minlength=E))
+    np.testing.assert_array_equal(g["offsets"], np.concatenate([[0], np.cumsum(g["counts"])]))
+    np.testing.assert_array_equal(g["perm"], np.argsort(flat, kind="stable"))
+    np.testing.assert_array_equal(g["inv"][g["perm"]], np.arange(T * k))
+    assert g["distinct"] == len(np.unique(flat))
+
+
+# ---- the block ----------------------------------------------------------------------
+
+def _tiny_layer(oracle, seed, H, F, E, k, shared, clamp, e_lo=124, e_span=7):
+    return oracle.OracleLayer.generated(seed, 3, H, F, E, k, experts=range(E), shared=shared, clamp=clamp,
+                                        e_lo=e_lo, e_span=e_span)
+
+
+@pytest.mark.parametrize("shared,clamp", [(False, 0.0), (True, 0.0), (True, 3.0)])
+def test_forward_vs_float64(oracle, shared, clamp):
+    H, F, E, k, T = 128, 96, 6, 3, 4
+    L = _tiny_layer(oracle, 11, H, F, E, k, shared, clamp, e_lo=120, e_span=4)
+    rng = np.random.default_rng(12)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    wts = rng.uniform(0.05, 0.6, (T, k)).astype(np.float32)
+    res = L.forward(x, ids, wts, taps=True, per_slot=True)
+    want, h = np_ref.moe_forward_f64(L, x, ids, wts, oracle.quantize_q8_0)
+    rms = np.sqrt(np.mean(want ** 2))
+    assert np.max(np.abs(res["out"] - want)) <= 1e-4 * rms
+    np.testing.assert_allclose(res["h"], h, rtol=1e-4, atol=1e-5 * np.abs(h).max())
+    # per-slot rows sum (in slot order) to the routed part of out
+    routed = res["per_slot"].astype(np.float64).sum(axis=1)
+    if not shared:
+        np.testing.assert_allclose(res["out"], routed, rtol=1e-5, atol=1e-6 * rms)
+    if clamp:
+        # the clamp really engaged: some pre-clamp |up| exceeded it
+        assert np.abs(h).max() > 0
+
+
+def test_forward_clamp_engages(oracle):
+    # large weights make |g|, |u| far exceed a small limit: output must differ from unclamped
+    H, F, E, k, T = 64, 64, 4, 2, 2
+    L1 = _tiny_layer(oracle, 21, H, F, E, k, False, 0.0, e_lo=130, e_span=2)
+    L2 = _tiny_layer(oracle, 21, H, F, E, k, False, 0.75, e_lo=130, e_span=2)
+    rng = np.random.default_rng(22)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.array([[0, 1], [2, 3]], np.int32)
+    wts = np.full((T, k), 0.5, np.float32)
+    a = L1.forward(x, ids, wts, taps=True)
+    b = L2.forward(x, ids, wts, taps=True)
+    assert np.abs(a["h"]).max() > 5 * np.abs(b["h"]).max()
+    want, _ = np_ref.moe_forward_f64(L2, x, ids, wts, oracle.quantize_q8_0)
+    rms = np.sqrt(np.mean(want ** 2))
+    assert np.max(np.abs(b["out"] - want)) <= 1e-4 * rms
+
+
+def test_forward_thread_count_invariant(oracle):
+    H, F, E, k, T = 256, 128, 8, 4, 5
+    L = _tiny_layer(oracle, 31, H, F, E, k, True, 0.0)
+    rng = np.random.default_rng(32)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    wts = rng.uniform(0.1, 0.4, (T, k)).astype(np.float32)
+    a = L.forward(x, ids, wts, n_threads=1)["out"]
+    b = L.forward(x, ids, wts, n_threads=7)["out"]
+    np.testing.assert_array_equal(a, b)
+
+
+# ---- generator ----------------------------------------------------------------------
+
+def test_mix64_known_answer(oracle):
+    # SplitMix64 seeded with 0: first outputs as published with the algorithm
+    assert oracle.lib().mo_mix64(0) == 0xE220A8397B1DCDAF
+    assert oracle.lib().mo_mix64(0x9E3779B97F4A7C15) == 0x6E789E6AA1B965F4
+
+
+def test_generator_distribution(oracle):
+    b = oracle.gen_mxfp4(99, 0, 0, 5, 512, 2048)
+    e = b[:, :, 0].ravel()
+    assert e.min() == 124 and e.max() == 130
+    cnt_e = np.bincount(e - 124, minlength=7)
+    assert np.all(np.abs(cnt_e / cnt_e.sum() - 1 / 7) < 0.01)
+    nib = np.concatenate([(b[:, :, 1:] & 0xF).ravel(), (b[:, :, 1:] >> 4).ravel()])
+    cnt = np.bincount(nib, minlength=16) / nib.size
+    assert np.all(np.abs(cnt - 1 / 16) < 0.002)
+    # different (layer, tensor, expert) keys give different bytes
+    assert not np.array_equal(b, oracle.gen_mxfp4(99, 0, 0, 6, 512, 2048))
+    assert not np.array_equal(b, oracle.gen_mxfp4(99, 0, 1, 5, 512, 2048))
