@@ -194,7 +194,30 @@ moe_status moe_graph_capture(moe_ctx *ctx, int n_layers, const int *layers,
 moe_status moe_graph_launch(moe_graph *g, void *stream);
 void moe_graph_destroy(moe_graph *g);
 
+/* ---- profiling ----------------------------------------------------------- */
+
+/* Per-kernel GPU time, from a HIP event pair recorded on the launch stream
+ * around every kernel the context launches while profiling is on (not under
+ * graph capture).  The reference keeps per-split phase timings the same way
+ * (moe-serv/src/moe_prof.h:36-137, MOESERV_PROFILE) and GPU timestamps
+ * around its dispatches (moe-serv/src/moe_probe_custom.cpp:411-475). */
+typedef struct {
+  const char *name;   /* kernel class, static string                        */
+  uint64_t launches;  /* launches timed since the last reset               */
+  double total_us;    /* summed event-to-event time                         */
+} moe_kernel_stat;
+
+moe_status moe_prof_enable(moe_ctx *ctx, int on);
+/* Wait for the recorded launches, add them up, and return one entry per
+ * kernel class with launches > 0 (at most cap, *n = the number of classes).
+ * reset != 0 clears the totals afterwards. */
+moe_status moe_prof_read(moe_ctx *ctx, moe_kernel_stat *stats, int cap, int *n, int reset);
+
 /* ---- test hooks ---------------------------------------------------------- */
+
+/* Keep the SwiGLU output h of every forward for moe_debug_last_h (off by
+ * default: it costs an extra f32 store per h value). */
+moe_status moe_debug_set_taps(moe_ctx *ctx, int on);
 
 /* Q8_0 of n floats (n % 32 == 0) with the kernels' own quantizer:
  * qs [n] int8, d [n/32] fp16 bits. */
@@ -205,7 +228,7 @@ moe_status moe_debug_quantize_q8_0(moe_ctx *ctx, const float *x_dev, int n,
 moe_status moe_debug_wave_sum(moe_ctx *ctx, const float *x_dev, int n_waves,
                               float *out_dev, void *stream);
 
-/* SwiGLU inputs/outputs of the last moe_forward on this context, for taps:
+/* SwiGLU output of the last moe_forward with taps on (moe_debug_set_taps):
  * h [rows][F] f32 before Q8_0, rows = T*k routed pairs in pair order, then
  * T shared rows.  Copies at most `cap` floats; returns the count in *n. */
 moe_status moe_debug_last_h(moe_ctx *ctx, float *h_host, size_t cap, size_t *n);

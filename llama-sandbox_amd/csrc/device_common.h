@@ -63,19 +63,16 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
-// Sum over all 64 lanes; every lane gets the total.
+__device__ __forceinline__ float readlane_f(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Sum over all 64 lanes; every lane gets the same total.  After row16_sum
+// every lane of a 16-lane row holds that row's sum; the four row sums are
+// read as scalars (lanes 0, 16, 32, 48) and added in a fixed order.
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);
-  // v_permlane16_swap: rows (0,1) and (2,3) of the two operands trade places;
-  // with both operands = v the two results add up to row0+row1 / row2+row3.
-  auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
-                                            __builtin_bit_cast(unsigned, v), false, false);
-  v = __builtin_bit_cast(float, p[0]) + __builtin_bit_cast(float, p[1]);
-  // v_permlane32_swap: the upper half of one operand trades with the lower
-  // half of the other; the two results add up to lanes 0-31 + lanes 32-63.
-  auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
-                                            __builtin_bit_cast(unsigned, v), false, false);
-  return __builtin_bit_cast(float, q[0]) + __builtin_bit_cast(float, q[1]);
+  return (readlane_f(v, 0) + readlane_f(v, 16)) + (readlane_f(v, 32) + readlane_f(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
@@ -83,12 +80,7 @@ __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp_f<0x4E>(v));
   v = fmaxf(v, dpp_f<0x141>(v));
   v = fmaxf(v, dpp_f<0x140>(v));
-  auto p = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
-                                            __builtin_bit_cast(unsigned, v), false, false);
-  v = fmaxf(__builtin_bit_cast(float, p[0]), __builtin_bit_cast(float, p[1]));
-  auto q = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
-                                            __builtin_bit_cast(unsigned, v), false, false);
-  return fmaxf(__builtin_bit_cast(float, q[0]), __builtin_bit_cast(float, q[1]));
+  return fmaxf(fmaxf(readlane_f(v, 0), readlane_f(v, 16)), fmaxf(readlane_f(v, 32), readlane_f(v, 48)));
 }
 
 // ---- Q8_0 ------------------------------------------------------------------

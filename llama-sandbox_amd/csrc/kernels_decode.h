@@ -139,7 +139,7 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
       float v = red_f[0];
       int i = red_i[0];
       for (int w = 1; w < 4; w++) argmax_merge(v, i, red_f[w], red_i[w]);
-      picked[s] = i;
+      picked[s] = i >= 0 ? i : 0;  // only NaN scores leave nothing selectable
     }
     __syncthreads();
   }
@@ -204,7 +204,10 @@ __global__ __launch_bounds__(256) void k_gu_decode(
     const int32_t *__restrict__ ids, int k, int shared_expert, int F, int KB, float clamp,
     uint32_t *__restrict__ hq, float *__restrict__ hd, float *__restrict__ htap) {
   const int s = blockIdx.y;
-  const int e = s < k ? ids[s] : shared_expert;
+  int e = s < k ? ids[s] : shared_expert;
+  // An id outside [0, E) reads no weights and yields h = 0 for its slot.
+  const bool valid = s >= k || (unsigned)e < (unsigned)shared_expert;
+  e = valid ? e : 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int r0 = blockIdx.x * 32 + wave * GU_ROWS_PER_WAVE;
 
@@ -221,7 +224,7 @@ __global__ __launch_bounds__(256) void k_gu_decode(
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int b = lane + 64 * j;
-      if (b < KB) {
+      if (valid && b < KB) {
         const uint4 wg = nib_g[rb + b];
         const uint4 wu = nib_u[rb + b];
         const uint32_t eg = sc_g[rb + b], eu = sc_u[rb + b];
@@ -269,7 +272,10 @@ __global__ __launch_bounds__(1024) void k_down_decode(
     const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int shared_expert,
     int S, int H, int KB, float *__restrict__ out, int per_slot) {
   const int s = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int e = s < k ? ids[s] : shared_expert;
+  int e = s < k ? ids[s] : shared_expert;
+  // An id outside [0, E) reads no weights and contributes 0.
+  const bool valid = s >= k || (unsigned)e < (unsigned)shared_expert;
+  e = valid ? e : 0;
   const int r0 = blockIdx.x * RD;
 
   uint32_t hr[NB][16];
@@ -286,7 +292,7 @@ __global__ __launch_bounds__(1024) void k_down_decode(
 #pragma unroll
     for (int j = 0; j < NB; j++) {
       const int b = lane + 64 * j;
-      if (b < KB) a = fmaf(scale_e8m0(hsc[j], sc_d[rb + b]), block_dot(nib_d[rb + b], hr[j]), a);
+      if (valid && b < KB) a = fmaf(scale_e8m0(hsc[j], sc_d[rb + b]), block_dot(nib_d[rb + b], hr[j]), a);
     }
     part[rr] = a;
   }

@@ -50,6 +50,7 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     const bool ok = e >= 0 && e < E;
     sid[p] = ok ? e : -1;
     if (ok) atomicAdd(&cnt[e], 1);
+    else if (inv) inv[p] = -1;  // dropped pair: no grouped row
   }
   __syncthreads();
   // exclusive scans over experts of the counts and of the "active" flags
@@ -78,11 +79,11 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
   if (tid < E) {
     counts[tid] = c;
     offsets[tid] = excl;
-    if (f) act[1 + exclf] = tid;
+    if (f && act) act[1 + exclf] = tid;
   }
   if (tid == 1023) {  // thread 1023's inclusive sums are the totals
     offsets[E] = base + v;
-    act[0] = basef + vf;
+    if (act) act[0] = basef + vf;
   }
   // stable placement: expert e's thread appends its pairs in pair order
   if (tid < E && c > 0) {
@@ -241,12 +242,20 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y,
   if (i >= (size_t)T * H) return;
   const int t = (int)(i / H), c = (int)(i % H);
   const int P = T * k;
+  // inv < 0 marks a pair whose expert id was out of range: it contributes 0.
   if (per_slot) {
-    for (int s = 0; s < k; s++) out[((size_t)t * k + s) * H + c] = y[(size_t)inv[t * k + s] * H + c];
+    for (int s = 0; s < k; s++) {
+      const int r = inv[t * k + s];
+      out[((size_t)t * k + s) * H + c] = r >= 0 ? y[(size_t)r * H + c] : 0.0f;
+    }
     return;
   }
-  float acc = y[(size_t)inv[t * k] * H + c];
-  for (int s = 1; s < k; s++) acc = __fadd_rn(acc, y[(size_t)inv[t * k + s] * H + c]);
+  const int r0 = inv[t * k];
+  float acc = r0 >= 0 ? y[(size_t)r0 * H + c] : 0.0f;
+  for (int s = 1; s < k; s++) {
+    const int r = inv[t * k + s];
+    acc = __fadd_rn(acc, r >= 0 ? y[(size_t)r * H + c] : 0.0f);
+  }
   if (shared) acc = __fadd_rn(acc, y[((size_t)P + t) * H + c]);
   out[i] = acc;
 }

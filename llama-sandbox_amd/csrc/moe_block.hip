@@ -57,6 +57,23 @@ struct scratch {
 
 }  // namespace
 
+// Kernel classes timed by the profiler (moe_prof_*), in the order of
+// kernel_names[].
+enum { K_QUANTIZE = 0, K_ROUTE, K_GROUP, K_GU_DECODE, K_DOWN_DECODE, K_GU_GROUPED, K_DOWN_GROUPED,
+       K_COMBINE, K_COUNT };
+static const char *const kernel_names[K_COUNT] = {
+    "quantize_q8_0", "route", "group", "gate_up_decode", "down_decode", "gate_up_grouped",
+    "down_grouped", "combine"};
+
+struct prof_state {
+  bool on = false;
+  struct rec { int kid; hipEvent_t a, b; };
+  std::vector<hipEvent_t> pool;  // idle events
+  std::vector<rec> pending;      // recorded, not yet read
+  uint64_t launches[K_COUNT] = {};
+  double total_us[K_COUNT] = {};
+};
+
 struct moe_ctx {
   int device = 0;
   uint64_t budget = 0, used = 0;
@@ -65,6 +82,49 @@ struct moe_ctx {
   std::string err;
   int inject = 0;  // bit 0: forward fails, bit 1: budget forced to 0
   bool capturing = false;
+  bool taps = false;  // keep the SwiGLU output h in sc.htap (moe_debug_set_taps)
+  prof_state prof;
+};
+
+// HIP-event pair around one kernel launch while profiling is on (never
+// under graph capture: a captured launch is timed by its replays instead).
+struct prof_scope {
+  moe_ctx *c;
+  int kid;
+  hipStream_t st;
+  hipEvent_t a = nullptr, b = nullptr;
+  static hipEvent_t take(prof_state &p) {
+    hipEvent_t e = nullptr;
+    if (!p.pool.empty()) {
+      e = p.pool.back();
+      p.pool.pop_back();
+    } else if (hipEventCreate(&e) != hipSuccess) {
+      e = nullptr;
+    }
+    return e;
+  }
+  prof_scope(moe_ctx *ctx, int k, hipStream_t s) : c(ctx), kid(k), st(s) {
+    if (!c->prof.on || c->capturing) return;
+    a = take(c->prof);
+    b = a ? take(c->prof) : nullptr;
+    if (a && b && hipEventRecord(a, st) != hipSuccess) {
+      c->prof.pool.push_back(a);
+      c->prof.pool.push_back(b);
+      a = b = nullptr;
+    } else if (a && !b) {
+      c->prof.pool.push_back(a);
+      a = nullptr;
+    }
+  }
+  ~prof_scope() {
+    if (!a) return;
+    if (hipEventRecord(b, st) == hipSuccess) {
+      c->prof.pending.push_back({kid, a, b});
+    } else {
+      c->prof.pool.push_back(a);
+      c->prof.pool.push_back(b);
+    }
+  }
 };
 
 struct moe_graph {
@@ -194,6 +254,11 @@ extern "C" void moe_ctx_destroy(moe_ctx *c) {
       if (m.sc) (void)hipFree(m.sc);
     }
   scratch_free(c->sc);
+  for (auto &r : c->prof.pending) {
+    (void)hipEventDestroy(r.a);
+    (void)hipEventDestroy(r.b);
+  }
+  for (hipEvent_t e : c->prof.pool) (void)hipEventDestroy(e);
   delete c;
 }
 
@@ -391,8 +456,11 @@ extern "C" moe_status moe_route(moe_ctx *c, const float *logits, const float *bi
       mode < 0 || mode > 2)
     return fail(c, MOE_ERR_INVALID_ARG, "moe_route: bad arguments");
   HIPC(c, hipSetDevice(c->device));
-  hipLaunchKernelGGL(k_route, dim3(T), dim3(256), 0, (hipStream_t)stream, logits, bias, E, k, mode, norm,
-                     scale, ids, wts);
+  {
+    prof_scope ps(c, K_ROUTE, (hipStream_t)stream);
+    hipLaunchKernelGGL(k_route, dim3(T), dim3(256), 0, (hipStream_t)stream, logits, bias, E, k, mode, norm,
+                       scale, ids, wts);
+  }
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
@@ -404,8 +472,11 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
       (long)T * k > MOE_GROUP_MAX_PAIRS)
     return fail(c, MOE_ERR_INVALID_ARG, "moe_group: bad arguments");
   HIPC(c, hipSetDevice(c->device));
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, counts, offsets,
-                     perm, inv, (int32_t *)nullptr);
+  {
+    prof_scope ps(c, K_GROUP, (hipStream_t)stream);
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, counts, offsets,
+                       perm, inv, (int32_t *)nullptr);
+  }
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
@@ -413,10 +484,10 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
 // The decode chain for T == 1.
 template <int NB>
 static void launch_gu_decode(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *ids,
-                             int k, int shared_expert) {
+                             int k, int shared_expert, float *htap) {
   hipLaunchKernelGGL(k_gu_decode<NB>, g, dim3(256), 0, st, L.m[T_GATE].nib, L.m[T_UP].nib, L.m[T_GATE].sc,
                      L.m[T_UP].sc, s.xq, s.xd, ids, k, shared_expert, L.d.ffn, L.d.hidden / 32, L.d.clamp,
-                     s.hq, s.hd, s.htap);
+                     s.hq, s.hd, htap);
 }
 
 template <int NB, int RD>
@@ -437,21 +508,29 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   const int nb_gu = ceil_div(KBh, 64), nb_dn = ceil_div(KBf, 64);
   if (S > 16 || nb_gu > 6 || nb_dn > 2) return fail(c, MOE_ERR_UNSUPPORTED, "decode: shape outside kernel range");
   scratch &s = c->sc;
-  hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div(KBh, 256)), dim3(256), 0, st, x, (uint32_t)KBh, s.xq, s.xd,
-                     (int8_t *)nullptr, (uint16_t *)nullptr);
-  const dim3 g(d.ffn / 32, S);
-  switch (nb_gu) {
-    case 1: launch_gu_decode<1>(g, st, L, s, ids, k, d.n_expert); break;
-    case 2: launch_gu_decode<2>(g, st, L, s, ids, k, d.n_expert); break;
-    case 3: launch_gu_decode<3>(g, st, L, s, ids, k, d.n_expert); break;
-    case 4: launch_gu_decode<4>(g, st, L, s, ids, k, d.n_expert); break;
-    case 5: launch_gu_decode<5>(g, st, L, s, ids, k, d.n_expert); break;
-    default: launch_gu_decode<6>(g, st, L, s, ids, k, d.n_expert); break;
+  float *htap = c->taps ? s.htap : nullptr;
+  {
+    prof_scope pq(c, K_QUANTIZE, st);
+    hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div(KBh, 256)), dim3(256), 0, st, x, (uint32_t)KBh, s.xq, s.xd,
+                       (int8_t *)nullptr, (uint16_t *)nullptr);
   }
-  s.h_rows = (size_t)S;
+  const dim3 g(d.ffn / 32, S);
+  {
+    prof_scope pg(c, K_GU_DECODE, st);
+    switch (nb_gu) {
+      case 1: launch_gu_decode<1>(g, st, L, s, ids, k, d.n_expert, htap); break;
+      case 2: launch_gu_decode<2>(g, st, L, s, ids, k, d.n_expert, htap); break;
+      case 3: launch_gu_decode<3>(g, st, L, s, ids, k, d.n_expert, htap); break;
+      case 4: launch_gu_decode<4>(g, st, L, s, ids, k, d.n_expert, htap); break;
+      case 5: launch_gu_decode<5>(g, st, L, s, ids, k, d.n_expert, htap); break;
+      default: launch_gu_decode<6>(g, st, L, s, ids, k, d.n_expert, htap); break;
+    }
+  }
+  s.h_rows = htap ? (size_t)S : 0;
   s.last_F = d.ffn;
   const int H = d.hidden;
   const int ps = per_slot ? 1 : 0;
+  prof_scope pd(c, K_DOWN_DECODE, st);
   if (nb_dn == 1) {
     if (H % 8 == 0) launch_down_decode<1, 8>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
     else if (H % 4 == 0) launch_down_decode<1, 4>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
@@ -468,10 +547,10 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
 // The grouped chain for T > 1.
 template <int NB>
 static void launch_gu_grouped(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *offsets,
-                              const int32_t *perm, const int32_t *act, int T, int shared) {
+                              const int32_t *perm, const int32_t *act, int T, int shared, float *htap) {
   hipLaunchKernelGGL(k_gu_grouped<NB>, g, dim3(256), 0, st, L.m[T_GATE].nib, L.m[T_UP].nib, L.m[T_GATE].sc,
                      L.m[T_UP].sc, s.xq, s.xd, offsets, perm, act, L.d.n_used, T, shared, L.d.n_expert,
-                     L.d.ffn, L.d.hidden / 32, L.d.clamp, s.hq, s.hd, s.htap);
+                     L.d.ffn, L.d.hidden / 32, L.d.clamp, s.hq, s.hd, htap);
 }
 
 template <int NB, int RD>
@@ -494,26 +573,42 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
     return fail(c, MOE_ERR_UNSUPPORTED, "grouped: shape outside kernel range");
   scratch &s = c->sc;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *act = inv + P;
-  hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div((long)T * KBh, 256)), dim3(256), 0, st, x, (uint32_t)(T * KBh),
-                     s.xq, s.xd, (int8_t *)nullptr, (uint16_t *)nullptr);
-  hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, ids, P, E, counts, offsets, perm, inv, act);
+  float *htap = c->taps ? s.htap : nullptr;
+  {
+    prof_scope pq(c, K_QUANTIZE, st);
+    hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div((long)T * KBh, 256)), dim3(256), 0, st, x,
+                       (uint32_t)(T * KBh), s.xq, s.xd, (int8_t *)nullptr, (uint16_t *)nullptr);
+  }
+  {
+    prof_scope pgr(c, K_GROUP, st);
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, ids, P, E, counts, offsets, perm, inv, act);
+  }
   const int ny = (P < E ? P : E) + shared;
   const dim3 ggu(d.ffn / 32, ny);
-  switch (nb_gu) {
-    case 1: launch_gu_grouped<1>(ggu, st, L, s, offsets, perm, act, T, shared); break;
-    case 2: launch_gu_grouped<2>(ggu, st, L, s, offsets, perm, act, T, shared); break;
-    case 3: launch_gu_grouped<3>(ggu, st, L, s, offsets, perm, act, T, shared); break;
-    case 4: launch_gu_grouped<4>(ggu, st, L, s, offsets, perm, act, T, shared); break;
-    case 5: launch_gu_grouped<5>(ggu, st, L, s, offsets, perm, act, T, shared); break;
-    default: launch_gu_grouped<6>(ggu, st, L, s, offsets, perm, act, T, shared); break;
+  {
+    prof_scope pg(c, K_GU_GROUPED, st);
+    switch (nb_gu) {
+      case 1: launch_gu_grouped<1>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
+      case 2: launch_gu_grouped<2>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
+      case 3: launch_gu_grouped<3>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
+      case 4: launch_gu_grouped<4>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
+      case 5: launch_gu_grouped<5>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
+      default: launch_gu_grouped<6>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
+    }
   }
-  s.h_rows = (size_t)P + (shared ? T : 0);
+  s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
   s.last_F = d.ffn;
   const dim3 gdn(d.hidden / 8, ny);
-  if (nb_dn == 1) launch_down_grouped<1, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
-  else launch_down_grouped<2, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
-  hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * d.hidden, 256)), dim3(256), 0, st, s.y, inv, T, k,
-                     d.hidden, shared, per_slot ? 1 : 0, out);
+  {
+    prof_scope pd(c, K_DOWN_GROUPED, st);
+    if (nb_dn == 1) launch_down_grouped<1, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
+    else launch_down_grouped<2, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
+  }
+  {
+    prof_scope pc(c, K_COMBINE, st);
+    hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * d.hidden, 256)), dim3(256), 0, st, s.y, inv, T, k,
+                       d.hidden, shared, per_slot ? 1 : 0, out);
+  }
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
@@ -633,7 +728,59 @@ extern "C" void moe_graph_destroy(moe_graph *g) {
 }
 
 // ---------------------------------------------------------------------------
+// profiling
+
+extern "C" moe_status moe_prof_enable(moe_ctx *c, int on) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  c->prof.on = on != 0;
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_prof_read(moe_ctx *c, moe_kernel_stat *stats, int cap, int *n, int reset) {
+  if (!c || !n || cap < 0 || (cap > 0 && !stats)) return fail(c, MOE_ERR_INVALID_ARG, "moe_prof_read: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  prof_state &p = c->prof;
+  moe_status st = MOE_OK;
+  for (auto &r : p.pending) {
+    float ms = 0.0f;
+    if (st == MOE_OK && (hipEventSynchronize(r.b) != hipSuccess || hipEventElapsedTime(&ms, r.a, r.b) != hipSuccess))
+      st = fail(c, MOE_ERR_HIP, "moe_prof_read: event query failed");
+    if (st == MOE_OK) {
+      p.launches[r.kid] += 1;
+      p.total_us[r.kid] += 1000.0 * (double)ms;
+    }
+    p.pool.push_back(r.a);
+    p.pool.push_back(r.b);
+  }
+  p.pending.clear();
+  int m = 0;
+  for (int k = 0; k < K_COUNT; k++) {
+    if (!p.launches[k]) continue;
+    if (m < cap) {
+      stats[m].name = kernel_names[k];
+      stats[m].launches = p.launches[k];
+      stats[m].total_us = p.total_us[k];
+    }
+    m++;
+  }
+  *n = m;
+  if (reset) {
+    for (int k = 0; k < K_COUNT; k++) {
+      p.launches[k] = 0;
+      p.total_us[k] = 0.0;
+    }
+  }
+  return st;
+}
+
+// ---------------------------------------------------------------------------
 // test hooks
+
+extern "C" moe_status moe_debug_set_taps(moe_ctx *c, int on) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  c->taps = on != 0;
+  return MOE_OK;
+}
 
 extern "C" moe_status moe_debug_quantize_q8_0(moe_ctx *c, const float *x, int n, int8_t *qs, uint16_t *d,
                                               void *stream) {

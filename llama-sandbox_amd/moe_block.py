@@ -38,6 +38,7 @@ EXPORTS = (
     "moe_ctx_reserve", "moe_layer_upload", "moe_layer_generate", "moe_layer_read_blocks",
     "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward", "moe_forward_host",
     "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
+    "moe_prof_enable", "moe_prof_read", "moe_debug_set_taps",
     "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
 )
 
@@ -56,6 +57,10 @@ class LayerDesc(ctypes.Structure):
     def of(cls, shape) -> "LayerDesc":
         return cls(shape.hidden, shape.ffn, shape.n_expert, shape.n_used, int(shape.has_shared),
                    float(shape.clamp))
+
+
+class KernelStat(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint64), ("total_us", ctypes.c_double)]
 
 
 _vp = ctypes.c_void_p
@@ -115,6 +120,13 @@ def load_library(path: str | None = None):
     L.moe_graph_launch.argtypes = [_vp, _vp]
     L.moe_graph_destroy.restype = None
     L.moe_graph_destroy.argtypes = [_vp]
+    L.moe_prof_enable.restype = st
+    L.moe_prof_enable.argtypes = [_vp, ctypes.c_int]
+    L.moe_prof_read.restype = st
+    L.moe_prof_read.argtypes = [_vp, ctypes.POINTER(KernelStat), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
+                                ctypes.c_int]
+    L.moe_debug_set_taps.restype = st
+    L.moe_debug_set_taps.argtypes = [_vp, ctypes.c_int]
     L.moe_debug_quantize_q8_0.restype = st
     L.moe_debug_quantize_q8_0.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp, _vp]
     L.moe_debug_wave_sum.restype = st
@@ -280,7 +292,21 @@ class MoeBlock:
                     "moe_graph_capture")
         return Graph(self, g.value, (xs, ids, wts, outs))
 
+    # -- profiling ----------------------------------------------------------------
+    def prof_enable(self, on: bool = True):
+        self._check(self.lib.moe_prof_enable(self.h, int(on)), "moe_prof_enable")
+
+    def prof_read(self, reset: bool = True) -> dict:
+        """{kernel class: (launches, total_us)} since the last reset."""
+        cap = 16
+        arr = (KernelStat * cap)()
+        n = ctypes.c_int()
+        self._check(self.lib.moe_prof_read(self.h, arr, cap, ctypes.byref(n), int(reset)), "moe_prof_read")
+        return {arr[i].name.decode(): (int(arr[i].launches), float(arr[i].total_us)) for i in range(min(n.value, cap))}
+
     # -- test hooks -------------------------------------------------------------
+    def set_taps(self, on: bool = True):
+        self._check(self.lib.moe_debug_set_taps(self.h, int(on)), "moe_debug_set_taps")
     def debug_quantize_q8_0(self, x, qs, d, stream=None):
         self._check(self.lib.moe_debug_quantize_q8_0(self.h, _ptr(x), x.numel(), _ptr(qs), _ptr(d),
                                                      _stream(stream)), "moe_debug_quantize_q8_0")

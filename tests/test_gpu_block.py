@@ -27,9 +27,22 @@ def rms(a):
 
 
 def assert_rms_close(got, ref, tol=TOL, what=""):
-    r = rms(ref)
-    err = float(np.max(np.abs(np.asarray(got, np.float64) - ref)))
-    say(f"{what} rms(ref)={r:.4e} max|diff|={err:.3e} ratio={err / r:.3e}")
+    """max|got - ref| <= tol * RMS(ref) over the finite outputs, and the same
+    outputs non-finite on both sides.  The synthetic weights (E8M0 up to 2^2,
+    codes up to 12) make |h| exceed 65504 * 127 for some tokens; Q8_0 stores
+    d = amax/127 as fp16 (ggml's block_q8_0), so d becomes inf and the down
+    rows of that slot inf/NaN, on the oracle exactly as in ggml-cpu."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    fin = np.isfinite(ref)
+    assert np.array_equal(np.isfinite(got), fin), f"{what}: non-finite outputs differ"
+    if not fin.any():
+        say(f"{what} all {ref.size} outputs non-finite on both sides")
+        return
+    r = rms(ref[fin])
+    err = float(np.max(np.abs(got[fin] - ref[fin])))
+    nf = int(ref.size - fin.sum())
+    say(f"{what} rms(ref)={r:.4e} max|diff|={err:.3e} ratio={err / r:.3e}" + (f" non-finite={nf}" if nf else ""))
     assert err <= tol * r, f"{what}: max|diff| {err:.3e} > {tol} * rms {r:.3e}"
 
 
@@ -43,6 +56,7 @@ def torch_dev():
 @pytest.fixture(scope="module")
 def blk(torch_dev):
     b = mb.MoeBlock(0)
+    b.set_taps(True)
     yield b
     b.close()
 
