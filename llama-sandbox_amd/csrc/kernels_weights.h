@@ -1,48 +1,69 @@
 // kernels_weights.h -- expert-weight residency kernels (device repack).
 //
-// Device layout of one expert matrix of R rows x K reduction (KB = K/32
-// blocks per row), for all experts of a layer back to back:
-//   nib[e][r][b] : uint4  -- the block's 16 nibble bytes, unchanged order
-//   sc [e][r][b] : uint8  -- the block's E8M0 exponent
-// i.e. ggml's 17-byte block split into a 16-byte-aligned nibble stream and a
-// separate exponent stream, so every weight load is one 128-bit coalesced
-// load (the reference splits the same two planes for the same reason,
-// moe-serv/src/moe_tp.h:235-278, in a column-interleaved order built for its
-// 4-column threads; here rows stay contiguous because a wave reads 64
-// consecutive blocks of one row).
+// ggml stores an expert matrix of R rows x K reduction as R*KB 17-byte
+// blocks {uint8 e; uint8 qs[16]} (KB = K/32), row-major.  On the device the
+// two parts are split into the row-interleaved layout the vecmat kernels
+// stream (kernels_rows.h):
+//   nib[grp][b][l]        uint4  qs of block b of row 64*grp + l (bytes unchanged)
+//   sc [grp][b/4][l][b%4] uint8  e  of the same block
+// for every row group grp = r/64 of every expert, experts back to back.
+// The reference splits the same two planes for the same reason
+// (moe-serv/src/moe_tp.h:235-278: nibble plane + scale plane, columns
+// interleaved for its column-per-thread kernel); here a lane owns a row and
+// a wave reads 64 rows' block b as one 1 KiB run.
+//
+// Every kernel below runs one thread per block of one expert matrix, indexed
+// by its position o in the device layout (so the device-side accesses are
+// coalesced), and maps it back to ggml's block index i = r*KB + b.
 #pragma once
 
 #include "device_common.h"
 
-// 17-byte blocks -> (nib, sc).  One thread per block.
-__global__ __launch_bounds__(256) void k_repack_blocks(const uint8_t *__restrict__ src,
-                                                       uint64_t n_blocks,
-                                                       uint4 *__restrict__ nib,
+__device__ __forceinline__ void layout_of(uint64_t o, int KB, uint64_t &i, uint64_t &sc_byte) {
+  const uint32_t l = (uint32_t)(o & 63u);
+  const uint64_t gb = o >> 6;  // grp*KB + b
+  const uint64_t g = gb / (uint64_t)KB;
+  const uint32_t b = (uint32_t)(gb - g * (uint64_t)KB);
+  const uint64_t r = g * 64u + l;
+  i = r * (uint64_t)KB + b;
+  sc_byte = ((g * (uint64_t)(KB / 4) + (b >> 2)) * 64u + l) * 4u + (b & 3u);
+}
+
+// ggml 17-byte blocks of consecutive expert matrices (per_exp = R*KB blocks
+// each, n_blocks in all) -> (nib, sc) of the same experts.
+__global__ __launch_bounds__(256) void k_repack_blocks(const uint8_t *__restrict__ src, uint64_t n_blocks,
+                                                       uint64_t per_exp, int KB, uint4 *__restrict__ nib,
                                                        uint8_t *__restrict__ sc) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i >= n_blocks) return;
+  const uint64_t o = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (o >= n_blocks) return;
+  const uint64_t e = o / per_exp, base = e * per_exp;
+  uint64_t i, sb;
+  layout_of(o - base, KB, i, sb);
+  i += base;
+  sb += base;
   const uint8_t *b = src + i * 17u;
   uint32_t w[4];
 #pragma unroll
   for (int d = 0; d < 4; d++) {
-    w[d] = (uint32_t)b[1 + 4 * d] | ((uint32_t)b[2 + 4 * d] << 8) |
-           ((uint32_t)b[3 + 4 * d] << 16) | ((uint32_t)b[4 + 4 * d] << 24);
+    w[d] = (uint32_t)b[1 + 4 * d] | ((uint32_t)b[2 + 4 * d] << 8) | ((uint32_t)b[3 + 4 * d] << 16) |
+           ((uint32_t)b[4 + 4 * d] << 24);
   }
-  nib[i] = make_uint4(w[0], w[1], w[2], w[3]);
-  sc[i] = b[0];
+  nib[o] = make_uint4(w[0], w[1], w[2], w[3]);
+  sc[sb] = b[0];
 }
 
-// Inverse: (nib, sc) -> 17-byte blocks.
+// Inverse: (nib, sc) of one matrix -> ggml 17-byte blocks.
 __global__ __launch_bounds__(256) void k_unpack_blocks(const uint4 *__restrict__ nib,
-                                                       const uint8_t *__restrict__ sc,
-                                                       uint64_t n_blocks,
-                                                       uint8_t *__restrict__ dst) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i >= n_blocks) return;
+                                                       const uint8_t *__restrict__ sc, uint64_t n_blocks,
+                                                       int KB, uint8_t *__restrict__ dst) {
+  const uint64_t o = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (o >= n_blocks) return;
+  uint64_t i, sb;
+  layout_of(o, KB, i, sb);
   uint8_t *b = dst + i * 17u;
-  const uint4 v = nib[i];
+  const uint4 v = nib[o];
   const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-  b[0] = sc[i];
+  b[0] = sc[sb];
 #pragma unroll
   for (int d = 0; d < 4; d++) {
 #pragma unroll
@@ -50,18 +71,19 @@ __global__ __launch_bounds__(256) void k_unpack_blocks(const uint4 *__restrict__
   }
 }
 
-// Counter-based synthetic MXFP4: block i of a matrix with key `key` has
+// Counter-based synthetic MXFP4: ggml block i of a matrix with key `key` has
 // nibble bytes = little-endian bytes of mix(key+2i+1), mix(key+2i+2) and
 // exponent e_lo + floor((mix(key ^ ~i) >> 32) * e_span / 2^32).
-__global__ __launch_bounds__(256) void k_generate_blocks(uint64_t key, uint64_t n_blocks,
-                                                         uint32_t e_lo, uint32_t e_span,
-                                                         uint4 *__restrict__ nib,
+__global__ __launch_bounds__(256) void k_generate_blocks(uint64_t key, uint64_t n_blocks, int KB, uint32_t e_lo,
+                                                         uint32_t e_span, uint4 *__restrict__ nib,
                                                          uint8_t *__restrict__ sc) {
-  const uint64_t i = (uint64_t)blockIdx.x * 256u + threadIdx.x;
-  if (i >= n_blocks) return;
+  const uint64_t o = (uint64_t)blockIdx.x * 256u + threadIdx.x;
+  if (o >= n_blocks) return;
+  uint64_t i, sb;
+  layout_of(o, KB, i, sb);
   const uint64_t a = mix64(key + 2u * i + 1u);
   const uint64_t b = mix64(key + 2u * i + 2u);
   const uint64_t c = mix64(key ^ ~i);
-  nib[i] = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
-  sc[i] = (uint8_t)(e_lo + (uint32_t)(((c >> 32) * (uint64_t)e_span) >> 32));
+  nib[o] = make_uint4((uint32_t)a, (uint32_t)(a >> 32), (uint32_t)b, (uint32_t)(b >> 32));
+  sc[sb] = (uint8_t)(e_lo + (uint32_t)(((c >> 32) * (uint64_t)e_span) >> 32));
 }

@@ -10,6 +10,7 @@
 #include "device_common.h"
 #include "kernels_decode.h"
 #include "kernels_group.h"
+#include "kernels_rows.h"
 #include "kernels_weights.h"
 
 #include <hip/hip_runtime.h>
@@ -26,9 +27,11 @@ namespace {
 
 enum { T_GATE = 0, T_UP = 1, T_DOWN = 2 };
 
+// One tensor of a layer (gate, up or down) for all E' = E + has_shared
+// experts, in the row-interleaved layout of kernels_weights.h.
 struct dev_mat {
-  uint4 *nib = nullptr;   // [E'][R][KB]
-  uint8_t *sc = nullptr;  // [E'][R][KB]
+  uint4 *nib = nullptr;   // E'*R*KB 16-byte nibble payloads
+  uint8_t *sc = nullptr;  // E'*R*KB E8M0 exponents
   int rows = 0, kb = 0;
 };
 
@@ -42,12 +45,17 @@ struct dev_layer {
 struct scratch {
   // sized for (T, H, F, E, k)
   int T = 0, H = 0, F = 0, E = 0, k = 0;
-  uint32_t *xq = nullptr; float *xd = nullptr;     // [T][H/32][16], [T][H/32]
   uint32_t *hq = nullptr; float *hd = nullptr;     // [P+T][F/32][16], [P+T][F/32]
   float *htap = nullptr;                           // [P+T][F]
   float *y = nullptr;                              // [P+T][H]
   int32_t *grp = nullptr;                          // grouping workspace
   size_t grp_words = 0;
+  // split-K decode: chunk partial sums and per-unit tickets (the tickets are
+  // zeroed once here and left at zero by every launch)
+  float *part = nullptr;
+  size_t part_floats = 0;
+  int32_t *ctr = nullptr;
+  size_t ctr_words = 0;
   // host-boundary staging
   float *x_in = nullptr; int32_t *ids_in = nullptr; float *wts_in = nullptr; float *out_buf = nullptr;
   size_t out_cap = 0;
@@ -59,10 +67,10 @@ struct scratch {
 
 // Kernel classes timed by the profiler (moe_prof_*), in the order of
 // kernel_names[].
-enum { K_QUANTIZE = 0, K_ROUTE, K_GROUP, K_GU_DECODE, K_DOWN_DECODE, K_GU_GROUPED, K_DOWN_GROUPED,
+enum { K_ROUTE = 0, K_GROUP, K_GU_DECODE, K_DOWN_DECODE, K_GU_GROUPED, K_DOWN_GROUPED,
        K_COMBINE, K_COUNT };
 static const char *const kernel_names[K_COUNT] = {
-    "quantize_q8_0", "route", "group", "gate_up_decode", "down_decode", "gate_up_grouped",
+    "route", "group", "gate_up_decode", "down_decode", "gate_up_grouped",
     "down_grouped", "combine"};
 
 struct prof_state {
@@ -76,6 +84,7 @@ struct prof_state {
 
 struct moe_ctx {
   int device = 0;
+  int n_cu = 256;
   uint64_t budget = 0, used = 0;
   std::map<int, dev_layer> layers;
   scratch sc;
@@ -166,8 +175,10 @@ static uint64_t host_mix64(uint64_t z) {
 }
 
 static bool desc_ok(const moe_layer_desc *d) {
+  // hidden and ffn are both a row count (multiple of 64 rows per lane group)
+  // and a reduction length (multiple of 4 blocks of 32 per exponent dword)
   return d && d->hidden > 0 && d->ffn > 0 && d->n_expert > 0 && d->n_used > 0 &&
-         d->hidden % 32 == 0 && d->ffn % 32 == 0 && d->n_used <= d->n_expert &&
+         d->hidden % 128 == 0 && d->ffn % 128 == 0 && d->n_used <= d->n_expert &&
          d->n_used <= 64 && d->n_expert <= MOE_ROUTE_MAX_E && (d->has_shared == 0 || d->has_shared == 1);
 }
 
@@ -182,7 +193,7 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 // scratch
 
 static void scratch_free(scratch &s) {
-  void *ptrs[] = {s.xq, s.xd, s.hq, s.hd, s.htap, s.y, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf};
+  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf, s.part, s.ctr};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   s = scratch();
@@ -190,7 +201,7 @@ static void scratch_free(scratch &s) {
 
 static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k) {
   scratch &s = c->sc;
-  if (s.xq && T <= s.T && H <= s.H && F <= s.F && E <= s.E && k <= s.k) return MOE_OK;
+  if (s.hq && T <= s.T && H <= s.H && F <= s.F && E <= s.E && k <= s.k) return MOE_OK;
   if (c->capturing) return fail(c, MOE_ERR_INVALID_ARG, "scratch too small under graph capture; call moe_ctx_reserve first");
   T = T > s.T ? T : s.T;
   H = H > s.H ? H : s.H;
@@ -200,8 +211,6 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipDeviceSynchronize());
   scratch_free(s);
   const size_t P = (size_t)T * k, R = P + T;
-  HIPC(c, hipMalloc(&s.xq, (size_t)T * (H / 32) * 64));
-  HIPC(c, hipMalloc(&s.xd, (size_t)T * (H / 32) * 4));
   HIPC(c, hipMalloc(&s.hq, R * (F / 32) * 64));
   HIPC(c, hipMalloc(&s.hd, R * (F / 32) * 4));
   HIPC(c, hipMalloc(&s.htap, R * F * 4));
@@ -213,6 +222,15 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipMalloc(&s.wts_in, P * 4));
   s.out_cap = P * H;
   HIPC(c, hipMalloc(&s.out_buf, s.out_cap * 4));
+  // decode partials: gate/up [S*G_F][C<=H/128][2][64], down [G_H][S][C<=F/128][64]
+  const size_t S1 = (size_t)k + 1;
+  const size_t p_gu = S1 * (F / 64) * (H / 128) * 128, p_dn = (size_t)(H / 64) * S1 * (F / 128) * 64;
+  s.part_floats = p_gu > p_dn ? p_gu : p_dn;
+  HIPC(c, hipMalloc(&s.part, s.part_floats * 4));
+  s.ctr_words = S1 * (F / 64) > (size_t)(H / 64) ? S1 * (F / 64) : (size_t)(H / 64);
+  HIPC(c, hipMalloc(&s.ctr, s.ctr_words * 4));
+  HIPC(c, hipMemset(s.ctr, 0, s.ctr_words * 4));
+  HIPC(c, hipDeviceSynchronize());
   s.T = T; s.H = H; s.F = F; s.E = E; s.k = k;
   return MOE_OK;
 }
@@ -238,6 +256,7 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
   if (hipSetDevice(device) != hipSuccess) return MOE_ERR_NO_DEVICE;
   moe_ctx *c = new moe_ctx;
   c->device = device;
+  c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
   c->budget = (inject & 2) ? 0 : budget_bytes;
   c->inject = inject;
   *out = c;
@@ -347,8 +366,14 @@ extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_de
   dev_layer *L = nullptr;
   moe_status st = layer_alloc(c, layer, d, &L);
   if (st != MOE_OK) return st;
-  // Stage 17-byte blocks through a bounded device buffer, repack on the device.
-  const size_t chunk_blocks = (size_t)1 << 22;  // 68 MiB of blocks per step
+  // Stage whole expert matrices of 17-byte blocks through a bounded device
+  // buffer (the layout interleaves the rows of an expert), repack on the device.
+  size_t max_per_exp = 0;
+  for (int t = 0; t < 3; t++) {
+    const size_t pe = (size_t)L->m[t].rows * L->m[t].kb;
+    max_per_exp = pe > max_per_exp ? pe : max_per_exp;
+  }
+  const size_t chunk_blocks = max_per_exp > ((size_t)1 << 22) ? max_per_exp : ((size_t)1 << 22);
   uint8_t *stage = nullptr;
   if (hipMalloc(&stage, chunk_blocks * 17) != hipSuccess) {
     layer_drop(c, layer);
@@ -358,18 +383,20 @@ extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_de
   for (int t = 0; t < 3 && st == MOE_OK; t++) {
     dev_mat &m = L->m[t];
     const size_t per_exp = (size_t)m.rows * m.kb;
+    const size_t batch = chunk_blocks / per_exp;  // experts per staged copy (>= 1)
     for (int part = 0; part < 1 + d->has_shared && st == MOE_OK; part++) {
       const uint8_t *host = (const uint8_t *)src[t][part];
-      const size_t nb = part == 0 ? per_exp * d->n_expert : per_exp;
+      const size_t n_exp = part == 0 ? (size_t)d->n_expert : 1;
       const size_t base = part == 0 ? 0 : per_exp * d->n_expert;
-      for (size_t off = 0; off < nb; off += chunk_blocks) {
-        const size_t n = nb - off < chunk_blocks ? nb - off : chunk_blocks;
+      for (size_t e0 = 0; e0 < n_exp; e0 += batch) {
+        const size_t ne = n_exp - e0 < batch ? n_exp - e0 : batch;
+        const size_t n = ne * per_exp, off = e0 * per_exp;
         if (hipMemcpy(stage, host + off * 17, n * 17, hipMemcpyHostToDevice) != hipSuccess) {
           st = fail(c, MOE_ERR_HIP, "moe_layer_upload: host->device copy failed");
           break;
         }
-        hipLaunchKernelGGL(k_repack_blocks, dim3(ceil_div((long)n, 256)), dim3(256), 0, 0, stage,
-                           (uint64_t)n, m.nib + base + off, m.sc + base + off);
+        hipLaunchKernelGGL(k_repack_blocks, dim3(ceil_div((long)n, 256)), dim3(256), 0, 0, stage, (uint64_t)n,
+                           (uint64_t)per_exp, m.kb, m.nib + base + off, m.sc + base + off);
       }
     }
   }
@@ -398,7 +425,7 @@ extern "C" moe_status moe_layer_generate(moe_ctx *c, int layer, const moe_layer_
                           (uint64_t)(uint32_t)expert;
       const uint64_t key = host_mix64(seed ^ host_mix64(id));
       hipLaunchKernelGGL(k_generate_blocks, dim3(ceil_div((long)per_exp, 256)), dim3(256), 0, 0, key,
-                         (uint64_t)per_exp, (uint32_t)e_lo, (uint32_t)e_span, m.nib + per_exp * e,
+                         (uint64_t)per_exp, m.kb, (uint32_t)e_lo, (uint32_t)e_span, m.nib + per_exp * e,
                          m.sc + per_exp * e);
     }
   }
@@ -422,7 +449,7 @@ extern "C" moe_status moe_layer_read_blocks(moe_ctx *c, int layer, int tensor, i
   uint8_t *tmp = nullptr;
   HIPC(c, hipMalloc(&tmp, nb * 17));
   hipLaunchKernelGGL(k_unpack_blocks, dim3(ceil_div((long)nb, 256)), dim3(256), 0, 0, m.nib + nb * expert,
-                     m.sc + nb * expert, (uint64_t)nb, tmp);
+                     m.sc + nb * expert, (uint64_t)nb, m.kb, tmp);
   hipError_t e = hipMemcpy(out, tmp, nb * 17, hipMemcpyDeviceToHost);
   (void)hipFree(tmp);
   if (e != hipSuccess) return fail(c, MOE_ERR_HIP, "moe_layer_read_blocks: copy failed");
@@ -481,128 +508,116 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
   return MOE_OK;
 }
 
-// The decode chain for T == 1.
-template <int NB>
-static void launch_gu_decode(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *ids,
-                             int k, int shared_expert, float *htap) {
-  hipLaunchKernelGGL(k_gu_decode<NB>, g, dim3(256), 0, st, L.m[T_GATE].nib, L.m[T_UP].nib, L.m[T_GATE].sc,
-                     L.m[T_UP].sc, s.xq, s.xd, ids, k, shared_expert, L.d.ffn, L.d.hidden / 32, L.d.clamp,
-                     s.hq, s.hd, htap);
+// Tokens per workgroup pass of the grouped kernels: as many as fit the
+// 64 KiB of LDS a workgroup can address without an attribute.
+static int pick_nt_gate_up(int H) {
+  if (gate_up_lds_bytes(H, 4) <= 65536) return 4;
+  if (gate_up_lds_bytes(H, 2) <= 65536) return 2;
+  return gate_up_lds_bytes(H, 1) <= 65536 ? 1 : 0;
+}
+static int pick_nt_down(int F) {
+  if (down_lds_bytes(F, 4) <= 65536) return 4;
+  if (down_lds_bytes(F, 2) <= 65536) return 2;
+  return down_lds_bytes(F, 1) <= 65536 ? 1 : 0;
 }
 
-template <int NB, int RD>
-static void launch_down_decode(int S, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *ids,
-                               const float *wts, int k, int shared_expert, float *out, int per_slot) {
-  hipLaunchKernelGGL((k_down_decode<NB, RD>), dim3(L.d.hidden / RD), dim3(64 * S), 0, st, L.m[T_DOWN].nib,
-                     L.m[T_DOWN].sc, s.hq, s.hd, ids, wts, k, shared_expert, S, L.d.hidden, L.d.ffn / 32, out,
-                     per_slot);
+// gate/up launch; grouped == 0: decode columns are slots (ids), one token.
+static void launch_gate_up(int NT, dim3 g, hipStream_t st, const dev_layer &L, const float *x, int grouped,
+                           const int32_t *ids, const int32_t *offsets, const int32_t *perm, const int32_t *act,
+                           int shared, int T, uint32_t *hq, float *hd, float *htap) {
+  const moe_layer_desc &d = L.d;
+  const size_t lds = gate_up_lds_bytes(d.hidden, NT);
+  const uint32_t *scg = reinterpret_cast<const uint32_t *>(L.m[T_GATE].sc);
+  const uint32_t *scu = reinterpret_cast<const uint32_t *>(L.m[T_UP].sc);
+#define MOE_GU_ARGS L.m[T_GATE].nib, L.m[T_UP].nib, scg, scu, x, grouped, ids, offsets, perm, act, d.n_used, \
+                    d.n_expert, shared, T, d.ffn, d.hidden, d.clamp, hq, hd, htap
+  if (NT == 4) hipLaunchKernelGGL(k_gate_up<4>, g, dim3(64 * MOE_GU_WAVES), lds, st, MOE_GU_ARGS);
+  else if (NT == 2) hipLaunchKernelGGL(k_gate_up<2>, g, dim3(64 * MOE_GU_WAVES), lds, st, MOE_GU_ARGS);
+  else hipLaunchKernelGGL(k_gate_up<1>, g, dim3(64 * MOE_GU_WAVES), lds, st, MOE_GU_ARGS);
+#undef MOE_GU_ARGS
 }
 
+static void launch_down(int NT, dim3 g, hipStream_t st, const dev_layer &L, const uint32_t *hq, const float *hd,
+                        int grouped, const int32_t *ids, const int32_t *offsets, const int32_t *perm,
+                        const int32_t *act, const float *wts, int shared, int T, float *y) {
+  const moe_layer_desc &d = L.d;
+  const size_t lds = down_lds_bytes(d.ffn, NT);
+  const uint32_t *scd = reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc);
+#define MOE_DN_ARGS L.m[T_DOWN].nib, scd, hq, hd, grouped, ids, offsets, perm, act, wts, d.n_used, d.n_expert, \
+                    shared, T, d.ffn, d.hidden, y
+  if (NT == 4) hipLaunchKernelGGL(k_down<4>, g, dim3(64 * MOE_DN_WAVES), lds, st, MOE_DN_ARGS);
+  else if (NT == 2) hipLaunchKernelGGL(k_down<2>, g, dim3(64 * MOE_DN_WAVES), lds, st, MOE_DN_ARGS);
+  else hipLaunchKernelGGL(k_down<1>, g, dim3(64 * MOE_DN_WAVES), lds, st, MOE_DN_ARGS);
+#undef MOE_DN_ARGS
+}
+
+// The decode chain for T == 1: split-K gate/up (+ SwiGLU and Q8_0 of h by
+// the last chunk of each row group), then split-K down with the router
+// weights and the slot-order combine done by the last chunk of each output
+// row group.  Two launches.
 static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
                                  float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
-  const int k = d.n_used;
+  const int k = d.n_used, E = d.n_expert, H = d.hidden, F = d.ffn;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
-  const int S = k + ((d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0);
-  const int KBh = d.hidden / 32, KBf = d.ffn / 32;
-  const int nb_gu = ceil_div(KBh, 64), nb_dn = ceil_div(KBf, 64);
-  if (S > 16 || nb_gu > 6 || nb_dn > 2) return fail(c, MOE_ERR_UNSUPPORTED, "decode: shape outside kernel range");
+  const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
+  const int S = k + shared;
   scratch &s = c->sc;
   float *htap = c->taps ? s.htap : nullptr;
-  {
-    prof_scope pq(c, K_QUANTIZE, st);
-    hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div(KBh, 256)), dim3(256), 0, st, x, (uint32_t)KBh, s.xq, s.xd,
-                       (int8_t *)nullptr, (uint16_t *)nullptr);
-  }
-  const dim3 g(d.ffn / 32, S);
+  const int KQh = H / 128, KQf = F / 128, Gf = F / MOE_RG, Gh = H / MOE_RG;
+  const int c1 = decode_chunks(S * Gf, KQh, c->n_cu), c2 = decode_chunks(Gh * S, KQf, c->n_cu);
+  if ((size_t)S * Gf * c1 * 128 > s.part_floats || (size_t)Gh * S * c2 * 64 > s.part_floats ||
+      (size_t)S * Gf > s.ctr_words || (size_t)Gh > s.ctr_words)
+    return fail(c, MOE_ERR_INVALID_ARG, "decode: scratch not sized for this shape");
+  const size_t lds1 = (size_t)4 * ((KQh + c1 - 1) / c1) * 68, lds2 = (size_t)4 * ((KQf + c2 - 1) / c2) * 68;
   {
     prof_scope pg(c, K_GU_DECODE, st);
-    switch (nb_gu) {
-      case 1: launch_gu_decode<1>(g, st, L, s, ids, k, d.n_expert, htap); break;
-      case 2: launch_gu_decode<2>(g, st, L, s, ids, k, d.n_expert, htap); break;
-      case 3: launch_gu_decode<3>(g, st, L, s, ids, k, d.n_expert, htap); break;
-      case 4: launch_gu_decode<4>(g, st, L, s, ids, k, d.n_expert, htap); break;
-      case 5: launch_gu_decode<5>(g, st, L, s, ids, k, d.n_expert, htap); break;
-      default: launch_gu_decode<6>(g, st, L, s, ids, k, d.n_expert, htap); break;
-    }
+    hipLaunchKernelGGL(k_gate_up_dec, dim3(S * Gf * c1), dim3(64), lds1, st, L.m[T_GATE].nib, L.m[T_UP].nib,
+                       reinterpret_cast<const uint32_t *>(L.m[T_GATE].sc),
+                       reinterpret_cast<const uint32_t *>(L.m[T_UP].sc), x, ids, k, E, F, H, c1, d.clamp, s.part,
+                       s.ctr, s.hq, s.hd, htap);
   }
   s.h_rows = htap ? (size_t)S : 0;
-  s.last_F = d.ffn;
-  const int H = d.hidden;
-  const int ps = per_slot ? 1 : 0;
-  prof_scope pd(c, K_DOWN_DECODE, st);
-  if (nb_dn == 1) {
-    if (H % 8 == 0) launch_down_decode<1, 8>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
-    else if (H % 4 == 0) launch_down_decode<1, 4>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
-    else return fail(c, MOE_ERR_UNSUPPORTED, "decode: hidden %% 4 != 0");
-  } else {
-    if (H % 8 == 0) launch_down_decode<2, 8>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
-    else if (H % 4 == 0) launch_down_decode<2, 4>(S, st, L, s, ids, wts, k, d.n_expert, out, ps);
-    else return fail(c, MOE_ERR_UNSUPPORTED, "decode: hidden %% 4 != 0");
+  s.last_F = F;
+  {
+    prof_scope pd(c, K_DOWN_DECODE, st);
+    hipLaunchKernelGGL(k_down_dec, dim3(Gh * S * c2), dim3(64), lds2, st, L.m[T_DOWN].nib,
+                       reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc), s.hq, s.hd, ids, wts, k, E, S, F, H, c2,
+                       per_slot ? 1 : 0, s.part, s.ctr, out);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
 
 // The grouped chain for T > 1.
-template <int NB>
-static void launch_gu_grouped(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s, const int32_t *offsets,
-                              const int32_t *perm, const int32_t *act, int T, int shared, float *htap) {
-  hipLaunchKernelGGL(k_gu_grouped<NB>, g, dim3(256), 0, st, L.m[T_GATE].nib, L.m[T_UP].nib, L.m[T_GATE].sc,
-                     L.m[T_UP].sc, s.xq, s.xd, offsets, perm, act, L.d.n_used, T, shared, L.d.n_expert,
-                     L.d.ffn, L.d.hidden / 32, L.d.clamp, s.hq, s.hd, htap);
-}
-
-template <int NB, int RD>
-static void launch_down_grouped(dim3 g, hipStream_t st, const dev_layer &L, const scratch &s,
-                                const int32_t *offsets, const int32_t *perm, const int32_t *act, const float *wts,
-                                int T, int shared) {
-  hipLaunchKernelGGL((k_down_grouped<NB, RD>), g, dim3(256), 0, st, L.m[T_DOWN].nib, L.m[T_DOWN].sc, s.hq, s.hd,
-                     offsets, perm, act, wts, L.d.n_used, T, shared, L.d.n_expert, L.d.hidden, L.d.ffn / 32, s.y);
-}
-
 static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
                                   int T, float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
   const int k = d.n_used, E = d.n_expert, P = T * k;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
   const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
-  const int KBh = d.hidden / 32, KBf = d.ffn / 32;
-  const int nb_gu = ceil_div(KBh, 64), nb_dn = ceil_div(KBf, 64);
-  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || nb_gu > 6 || nb_dn > 2 || d.hidden % 8)
+  const int nt_gu = pick_nt_gate_up(d.hidden), nt_dn = pick_nt_down(d.ffn);
+  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || !nt_gu || !nt_dn)
     return fail(c, MOE_ERR_UNSUPPORTED, "grouped: shape outside kernel range");
   scratch &s = c->sc;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *act = inv + P;
   float *htap = c->taps ? s.htap : nullptr;
   {
-    prof_scope pq(c, K_QUANTIZE, st);
-    hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div((long)T * KBh, 256)), dim3(256), 0, st, x,
-                       (uint32_t)(T * KBh), s.xq, s.xd, (int8_t *)nullptr, (uint16_t *)nullptr);
-  }
-  {
     prof_scope pgr(c, K_GROUP, st);
     hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, ids, P, E, counts, offsets, perm, inv, act);
   }
   const int ny = (P < E ? P : E) + shared;
-  const dim3 ggu(d.ffn / 32, ny);
   {
     prof_scope pg(c, K_GU_GROUPED, st);
-    switch (nb_gu) {
-      case 1: launch_gu_grouped<1>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
-      case 2: launch_gu_grouped<2>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
-      case 3: launch_gu_grouped<3>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
-      case 4: launch_gu_grouped<4>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
-      case 5: launch_gu_grouped<5>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
-      default: launch_gu_grouped<6>(ggu, st, L, s, offsets, perm, act, T, shared, htap); break;
-    }
+    launch_gate_up(nt_gu, dim3(d.ffn / MOE_RG, ny), st, L, x, 1, ids, offsets, perm, act, shared, T, s.hq, s.hd,
+                   htap);
   }
   s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
   s.last_F = d.ffn;
-  const dim3 gdn(d.hidden / 8, ny);
   {
     prof_scope pd(c, K_DOWN_GROUPED, st);
-    if (nb_dn == 1) launch_down_grouped<1, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
-    else launch_down_grouped<2, 8>(gdn, st, L, s, offsets, perm, act, wts, T, shared);
+    launch_down(nt_dn, dim3(d.hidden / MOE_RG, ny), st, L, s.hq, s.hd, 1, ids, offsets, perm, act, wts, shared, T,
+                s.y);
   }
   {
     prof_scope pc(c, K_COMBINE, st);
@@ -677,7 +692,7 @@ extern "C" moe_status moe_graph_capture(moe_ctx *c, int n_layers, const int *lay
     if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layers[i]);
     const moe_layer_desc &d = it->second.d;
     const scratch &s = c->sc;
-    if (!s.xq || T > s.T || d.hidden > s.H || d.ffn > s.F || d.n_expert > s.E || d.n_used > s.k)
+    if (!s.hq || T > s.T || d.hidden > s.H || d.ffn > s.F || d.n_expert > s.E || d.n_used > s.k)
       return fail(c, MOE_ERR_INVALID_ARG, "moe_graph_capture: call moe_ctx_reserve for this shape first");
   }
   HIPC(c, hipSetDevice(c->device));
@@ -788,16 +803,8 @@ extern "C" moe_status moe_debug_quantize_q8_0(moe_ctx *c, const float *x, int n,
   if (!x || !qs || !d || n <= 0 || n % 32) return fail(c, MOE_ERR_INVALID_ARG, "moe_debug_quantize_q8_0: bad arguments");
   HIPC(c, hipSetDevice(c->device));
   const int nb = n / 32;
-  uint32_t *tq = nullptr;
-  float *td = nullptr;
-  HIPC(c, hipMalloc(&tq, (size_t)nb * 64));
-  HIPC(c, hipMalloc(&td, (size_t)nb * 4));
-  hipLaunchKernelGGL(k_quantize_q8, dim3(ceil_div(nb, 256)), dim3(256), 0, (hipStream_t)stream, x, (uint32_t)nb,
-                     tq, td, qs, d);
-  hipError_t e = hipStreamSynchronize((hipStream_t)stream);
-  (void)hipFree(tq);
-  (void)hipFree(td);
-  if (e != hipSuccess) return fail(c, MOE_ERR_HIP, "moe_debug_quantize_q8_0 failed");
+  hipLaunchKernelGGL(k_debug_quantize, dim3(ceil_div(nb, 64)), dim3(64), 0, (hipStream_t)stream, x, nb, qs, d);
+  HIPC(c, hipGetLastError());
   return MOE_OK;
 }
 
