@@ -402,13 +402,13 @@ __global__ __launch_bounds__(64 * MOE_DN_WAVES) void k_down(
 }
 
 // ---------------------------------------------------------------------------
-// Decode (T == 1) as split-K one-wave workgroups.
+// Decode gate/up (T == 1) as split-K one-wave workgroups.
 //
 // A decode call is small (the 9 touched experts of a V3 layer) and HBM-bound
 // only if every CU streams the same share: a workgroup per (slot, row group)
 // leaves the chip unevenly loaded (288 units on 256 CUs).  So the reduction
 // K of every (slot, row group) unit is cut into C chunks, one single-wave
-// workgroup each (2304 equal workgroups for V3 gate/up, 2016 for down).
+// workgroup each (2304 equal workgroups for V3 gate/up).
 // Each writes its 64 partial sums; the last workgroup of a unit to finish
 // adds the chunks in chunk order and finishes the unit, then resets the
 // ticket for the next call.  No workgroup ever waits on another, and the
@@ -428,13 +428,14 @@ __device__ __forceinline__ void store_shared(float *p, float v) {
   __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// All of this wave's stores complete, then one lane takes a ticket; every
-// lane gets the ticket's previous value.
+// All of this wave's stores complete, then lane 0 takes a ticket; the
+// ticket's previous value is returned wave-uniform (an SGPR via readfirstlane,
+// read while every lane is active), so branches on it are scalar branches.
 __device__ __forceinline__ int ticket_take(int32_t *ctr, int lane) {
   __builtin_amdgcn_s_waitcnt(0);
   int t = 0;
   if (lane == 0) t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __shfl(t, 0);
+  return __builtin_amdgcn_readfirstlane(t);
 }
 
 __device__ __forceinline__ float load_acquired(const float *p) {
@@ -502,51 +503,125 @@ __global__ __launch_bounds__(64) void k_gate_up_dec(
   if (htap) htap[(size_t)s * F + (size_t)g * MOE_RG + lane] = h;
 }
 
-// down x router weight, slot-order combine.  grid G*S*C (G = H/64), 64
-// threads; block id = (g*S + s)*C + c.  part: [G][S][C][64] f32, ctr: [G].
-// out [H] = ((y_0 + y_1) + ...) + y_shared, y_s = (sum of s's chunks) * w_s
-// (the reference's MUL node and trunk ADD chain); per_slot: out[s][H] = y_s.
-__global__ __launch_bounds__(64) void k_down_dec(
+// Decode down with the top-k combine fused (T == 1).  grid H/16, 64*S
+// threads: wave s computes slot s (s == k: the shared expert) for 16 output
+// rows; lane = (row r16 = lane & 15, K-quarter kq = lane >> 4), quarter kq
+// takes the 4-block groups g = 4j + kq.  The quarters are summed with two
+// lane swaps, each slot's rows are scaled by its router weight, and the
+// slots are added in slot order, ((y0 + y1) + ...) + shared (the
+// reference's trunk ADD chain, nano-glm/lib/models/glm_dsa/moe_block.h:120-131).
+// per_slot: out[s][H] = y_s (the MUL node of the reference's split) instead.
+// A 16-row workgroup reads 256 B runs of every 1 KiB block row (the layout's
+// 64-row groups); all slots of a row live in one workgroup, so nothing
+// crosses workgroups.  LDS: per slot KQ groups of 272 B (4 h blocks + 16 B so
+// the four quarters' reads fall in different banks) + KB scales, then the
+// [S][16] slot rows.
+#define MOE_DN_GROUP_BYTES 272
+
+__device__ __forceinline__ void dq_load(wgroup<1> &g, const uint4 *__restrict__ nib, const uint32_t *__restrict__ sc,
+                                        int grp, int lane64) {
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+    g.w[0][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(nib + (size_t)(4 * grp + i) * MOE_RG + lane64));
+  g.e[0] = __builtin_nontemporal_load(sc + (size_t)grp * MOE_RG + lane64);
+}
+
+__global__ __launch_bounds__(1024) void k_down_decode(
     const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hq,
     const float *__restrict__ hd, const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int E,
-    int S, int F, int H, int C, int per_slot, float *__restrict__ part, int32_t *__restrict__ ctr,
-    float *__restrict__ out) {
+    int S, int F, int H, int per_slot, float *__restrict__ out) {
   extern __shared__ __align__(16) uint32_t lds[];
-  const int KB = F / MOE_QK, KQ = KB / 4, G = H / MOE_RG;
-  const int lane = threadIdx.x;
-  const int r = blockIdx.x / C, c = blockIdx.x - r * C;
-  const int g = r / S, s = r - g * S;
+  const int KB = F / MOE_QK, KQ = KB / 4;
+  const int lane = threadIdx.x & 63, s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int r16 = lane & 15, kq = lane >> 4;
+  const size_t slot_bytes = (size_t)KQ * MOE_DN_GROUP_BYTES + (size_t)KB * 4;
+  uint8_t *base = reinterpret_cast<uint8_t *>(lds) + (size_t)s * slot_bytes;
+  float *d_s = reinterpret_cast<float *>(base + (size_t)KQ * MOE_DN_GROUP_BYTES);
+  float *ys = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + (size_t)S * slot_bytes);  // [S][16]
+
   int e = s < k ? ids[s] : E;
-  const bool valid = s >= k || (unsigned)e < (unsigned)E;
+  const bool valid = s >= k || (unsigned)e < (unsigned)E;  // an out-of-range id reads nothing, yields 0
   e = valid ? e : 0;
-  int q0, q1;
-  wave_groups(KQ, C, c, q0, q1);
-  const int nq = q1 - q0;
-  const size_t grp = (size_t)e * G + g;
-  const uint4 *const nibs[1] = {nib_d + (grp * KB + 4 * q0) * MOE_RG};
-  const uint32_t *const scs[1] = {sc_d + (grp * KQ + q0) * MOE_RG};
-  wgroup<1> ring[MOE_DEC_DEPTH + 1];
-  ring_prime<1, MOE_DEC_DEPTH + 1>(ring, nibs, scs, nq, lane);
-  uint32_t *q_s = lds;
-  float *d_s = reinterpret_cast<float *>(lds + (size_t)4 * nq * 16);
-  stage_copy(hq + ((size_t)s * KB + 4 * q0) * 16, hd + (size_t)s * KB + 4 * q0, 4 * nq, q_s, d_s, lane);
-  __syncthreads();
-  float acc[1][1];
-  rows_dot<1, 1, MOE_DEC_DEPTH + 1>(ring, nibs, scs, nq, q_s, d_s, 0, lane, acc);
-  store_shared(part + (((size_t)g * S + s) * C + c) * MOE_RG + lane, valid ? acc[0][0] : 0.0f);
-  if (ticket_take(ctr + g, lane) != S * C - 1) return;
-  // last of this row group: every slot's chunks in order, weight, slot order
-  const float *pg = part + (size_t)g * S * C * MOE_RG;
-  float o = 0.0f;
-  for (int ss = 0; ss < S; ss++) {
-    float y = 0.0f;
-    for (int cc = 0; cc < C; cc++) y += load_acquired(pg + ((size_t)ss * C + cc) * MOE_RG + lane);
-    if (ss < k) y = __fmul_rn(y, wts[ss]);
-    if (per_slot) out[(size_t)ss * H + (size_t)g * MOE_RG + lane] = y;
-    else o = ss == 0 ? y : __fadd_rn(o, y);
+  const int G = H / MOE_RG;
+  const int grp64 = blockIdx.x >> 2, lane64 = (blockIdx.x & 3) * 16 + r16;
+  const size_t mg = (size_t)e * G + grp64;
+  const uint4 *nib = nib_d + mg * KB * MOE_RG;
+  const uint32_t *sc = sc_d + mg * KQ * MOE_RG;
+  const int nj = (KQ + 3) / 4;
+
+  // first weight group in flight before the h staging
+  wgroup<1> ga, gb;
+  dq_load(ga, nib, sc, kq < KQ ? kq : KQ - 1, lane64);
+  // stage h of this slot: block b -> group b/4 at 272 B, offset (b%4)*64
+  const uint4 *hsrc = reinterpret_cast<const uint4 *>(hq + (size_t)s * KB * 16);
+  const int n16 = KB * 4;  // 16-byte pieces of this slot's h
+  for (int i0 = 0; i0 < n16; i0 += 256) {
+    uint32_t off[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {  // a piece past the end lands in group 0's (unread) pad
+      const int i = i0 + 64 * r + lane;
+      const int b = i >> 2, part = i & 3;
+      off[r] = i < n16 ? (uint32_t)((b >> 2) * MOE_DN_GROUP_BYTES + (b & 3) * 64 + part * 16) : 256u;
+    }
+    uint4 v[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {  // all four loads in flight, clamped in range
+      const int i = i0 + 64 * r + lane;
+      v[r] = hsrc[i < n16 ? i : n16 - 1];
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int r = 0; r < 4; r++) *reinterpret_cast<uint4 *>(base + off[r]) = v[r];
   }
-  if (!per_slot) out[(size_t)g * MOE_RG + lane] = o;
-  if (lane == 0) __hip_atomic_store(ctr + g, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int b = lane; b < KB; b += 64) d_s[b] = hd[(size_t)s * KB + b];
+  __syncthreads();
+
+  float acc = 0.0f;
+  for (int j = 0;; j += 2) {
+    const int g0 = 4 * j + kq, g1 = 4 * j + 4 + kq, g2 = 4 * j + 8 + kq;
+    dq_load(gb, nib, sc, g1 < KQ ? g1 : KQ - 1, lane64);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      float a[1][1];
+      a[0][0] = 0.0f;
+      dot_group<1, 1>(ga, 0, reinterpret_cast<const uint32_t *>(base + (size_t)(g0 < KQ ? g0 : 0) * MOE_DN_GROUP_BYTES),
+                      d_s + 4 * (g0 < KQ ? g0 : 0), 0, a);
+      acc += g0 < KQ ? a[0][0] : 0.0f;
+    }
+    if (j + 1 >= nj) break;
+    dq_load(ga, nib, sc, g2 < KQ ? g2 : KQ - 1, lane64);
+    __builtin_amdgcn_sched_barrier(0);
+    {
+      float a[1][1];
+      a[0][0] = 0.0f;
+      dot_group<1, 1>(gb, 0, reinterpret_cast<const uint32_t *>(base + (size_t)(g1 < KQ ? g1 : 0) * MOE_DN_GROUP_BYTES),
+                      d_s + 4 * (g1 < KQ ? g1 : 0), 0, a);
+      acc += g1 < KQ ? a[0][0] : 0.0f;
+    }
+    if (j + 2 >= nj) break;
+  }
+  // sum the four K-quarters: (q0 + q1) + (q2 + q3) in every quarter's lanes
+  acc += __shfl_xor(acc, 16);
+  acc += __shfl_xor(acc, 32);
+  float v = valid ? acc : 0.0f;
+  if (s < k) v = __fmul_rn(v, wts[s]);
+  const int row = blockIdx.x * 16 + r16;
+  if (per_slot) {
+    if (lane < 16) out[(size_t)s * H + row] = v;
+    return;
+  }
+  if (lane < 16) ys[s * 16 + lane] = v;
+  __syncthreads();
+  if (threadIdx.x < 16) {
+    float o = ys[threadIdx.x];
+    for (int q = 1; q < S; q++) o = __fadd_rn(o, ys[q * 16 + threadIdx.x]);
+    out[blockIdx.x * 16 + threadIdx.x] = o;
+  }
+}
+
+static inline size_t down_decode_lds_bytes(int F, int S) {
+  const int KB = F / MOE_QK, KQ = KB / 4;
+  return (size_t)S * ((size_t)KQ * MOE_DN_GROUP_BYTES + (size_t)KB * 4) + (size_t)S * 16 * 4;
 }
 
 // Chunks per unit for the split-K decode kernels: about 9 single-wave

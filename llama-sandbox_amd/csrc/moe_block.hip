@@ -52,7 +52,7 @@ struct scratch {
   size_t grp_words = 0;
   // split-K decode: chunk partial sums and per-unit tickets (the tickets are
   // zeroed once here and left at zero by every launch)
-  float *part = nullptr;
+  float *part = nullptr;   // split-K gate/up partials
   size_t part_floats = 0;
   int32_t *ctr = nullptr;
   size_t ctr_words = 0;
@@ -222,12 +222,12 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipMalloc(&s.wts_in, P * 4));
   s.out_cap = P * H;
   HIPC(c, hipMalloc(&s.out_buf, s.out_cap * 4));
-  // decode partials: gate/up [S*G_F][C<=H/128][2][64], down [G_H][S][C<=F/128][64]
+  // decode gate/up partials: [S*G_F][C<=H/128][2][64]
   const size_t S1 = (size_t)k + 1;
-  const size_t p_gu = S1 * (F / 64) * (H / 128) * 128, p_dn = (size_t)(H / 64) * S1 * (F / 128) * 64;
-  s.part_floats = p_gu > p_dn ? p_gu : p_dn;
+  s.part_floats = S1 * (F / 64) * (H / 128) * 128;
   HIPC(c, hipMalloc(&s.part, s.part_floats * 4));
-  s.ctr_words = S1 * (F / 64) > (size_t)(H / 64) ? S1 * (F / 64) : (size_t)(H / 64);
+  // tickets: one per (slot, 64-row group of F)
+  s.ctr_words = S1 * (F / 64);
   HIPC(c, hipMalloc(&s.ctr, s.ctr_words * 4));
   HIPC(c, hipMemset(s.ctr, 0, s.ctr_words * 4));
   HIPC(c, hipDeviceSynchronize());
@@ -257,6 +257,7 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
   moe_ctx *c = new moe_ctx;
   c->device = device;
   c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
+
   c->budget = (inject & 2) ? 0 : budget_bytes;
   c->inject = inject;
   *out = c;
@@ -551,10 +552,10 @@ static void launch_down(int NT, dim3 g, hipStream_t st, const dev_layer &L, cons
 #undef MOE_DN_ARGS
 }
 
-// The decode chain for T == 1: split-K gate/up (+ SwiGLU and Q8_0 of h by
-// the last chunk of each row group), then split-K down with the router
-// weights and the slot-order combine done by the last chunk of each output
-// row group.  Two launches.
+// The decode chain for T == 1, two launches: split-K gate/up (+ SwiGLU and
+// Q8_0 of h by the last chunk of each row group), then down with the router
+// weights and the slot-order combine fused (all slots of 16 output rows per
+// workgroup).
 static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
                                  float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
@@ -564,12 +565,12 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   const int S = k + shared;
   scratch &s = c->sc;
   float *htap = c->taps ? s.htap : nullptr;
-  const int KQh = H / 128, KQf = F / 128, Gf = F / MOE_RG, Gh = H / MOE_RG;
-  const int c1 = decode_chunks(S * Gf, KQh, c->n_cu), c2 = decode_chunks(Gh * S, KQf, c->n_cu);
-  if ((size_t)S * Gf * c1 * 128 > s.part_floats || (size_t)Gh * S * c2 * 64 > s.part_floats ||
-      (size_t)S * Gf > s.ctr_words || (size_t)Gh > s.ctr_words)
+  const int KQh = H / 128, Gf = F / MOE_RG;
+  const int c1 = decode_chunks(S * Gf, KQh, c->n_cu);
+  if ((size_t)S * Gf * c1 * 128 > s.part_floats || (size_t)S * Gf > s.ctr_words)
     return fail(c, MOE_ERR_INVALID_ARG, "decode: scratch not sized for this shape");
-  const size_t lds1 = (size_t)4 * ((KQh + c1 - 1) / c1) * 68, lds2 = (size_t)4 * ((KQf + c2 - 1) / c2) * 68;
+  const size_t lds1 = (size_t)4 * ((KQh + c1 - 1) / c1) * 68, lds2 = down_decode_lds_bytes(F, S);
+  if (S > 16 || lds2 > 65536) return fail(c, MOE_ERR_UNSUPPORTED, "decode: more than 16 slots or ffn too large");
   {
     prof_scope pg(c, K_GU_DECODE, st);
     hipLaunchKernelGGL(k_gate_up_dec, dim3(S * Gf * c1), dim3(64), lds1, st, L.m[T_GATE].nib, L.m[T_UP].nib,
@@ -581,9 +582,9 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   s.last_F = F;
   {
     prof_scope pd(c, K_DOWN_DECODE, st);
-    hipLaunchKernelGGL(k_down_dec, dim3(Gh * S * c2), dim3(64), lds2, st, L.m[T_DOWN].nib,
-                       reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc), s.hq, s.hd, ids, wts, k, E, S, F, H, c2,
-                       per_slot ? 1 : 0, s.part, s.ctr, out);
+    hipLaunchKernelGGL(k_down_decode, dim3(H / 16), dim3(64 * S), lds2, st, L.m[T_DOWN].nib,
+                       reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc), s.hq, s.hd, ids, wts, k, E, S, F, H,
+                       per_slot ? 1 : 0, out);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
