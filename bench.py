@@ -1,5 +1,5 @@
 #!/usr/bin/env python3
-"""Benchmark of the gfx950 MoE block on BASELINE.json's headline workload.
+"""Benchmark of the gfx950 MoE block on the headline decode workload.
 
 Workload (config C2): one DeepSeek-V3-shaped MoE layer at 1-token decode --
 hidden 7168, expert FFN 2048, 256 routed experts + 1 shared expert of the same
@@ -51,7 +51,40 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cpus))")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the hipGraph")
+    ap.add_argument("--copy-mib", type=int, default=0,
+                    help="only run a plain device-to-device copy of this many MiB three times (the reference "
+                         "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
     return ap.parse_args()
+
+
+def copy_calibration(mib: int):
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda:0")
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    for i in range(3):
+        t = time.perf_counter()
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copy {mib} MiB: {(time.perf_counter() - t) * 1e6:.1f} us")
+    print(json.dumps({"copy_mib": mib, "bytes_read": n * 4, "bytes_written": n * 4}), flush=True)
+
+
+def profiled_traffic(kernel_class: str):
+    """HBM bytes per launch of `kernel_class` from the committed rocprofv3
+    counter summary (profiles/*.md lines 'traffic_bytes_per_launch <class>
+    <bytes>', FETCH_SIZE + WRITE_SIZE scaled by a copy-kernel calibration),
+    or None if no summary covers it."""
+    import glob
+
+    for path in sorted(glob.glob(os.path.join(REPO, "profiles", "*.md"))):
+        for line in open(path):
+            f = line.split()
+            if len(f) == 3 and f[0] == "traffic_bytes_per_launch" and f[1] == kernel_class:
+                return int(f[2])
+    return None
 
 
 def cpu_baseline(seconds: float, threads: int, seed: int):
@@ -93,6 +126,9 @@ def cpu_baseline(seconds: float, threads: int, seed: int):
 
 def main():
     args = parse()
+    if args.copy_mib > 0:
+        copy_calibration(args.copy_mib)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               f"sharding of the block is design-only", file=sys.stderr)
@@ -239,7 +275,7 @@ def main():
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": profiled_traffic(dominant),
             "bytes_per_launch": round(per_kernel[dominant]),
             "avg_launch_us": round(dom_us, 3),
         },

@@ -107,7 +107,7 @@ struct prof_scope {
     if (!p.pool.empty()) {
       e = p.pool.back();
       p.pool.pop_back();
-    } else if (hipEventCreate(&e) != hipSuccess) {
+    } else if (hipEventCreateWithFlags(&e, hipEventDisableSystemFence) != hipSuccess) {  // timing only: no cache flush
       e = nullptr;
     }
     return e;
