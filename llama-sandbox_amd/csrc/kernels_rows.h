@@ -1,60 +1,86 @@
-// kernels_rows.h -- the expert vecmat kernels (decode and small-batch grouped).
+// kernels_rows.h -- the expert kernels (decode and grouped), on gfx950's
+// scaled MFMA: v_mfma_scale_f32_16x16x128_f8f6f4 with the MXFP4 weights as
+// the fp4 A operand (their E8M0 exponents as the A scales) and the Q8_0
+// activations as the fp8 B operand.
 //
-// Weight layout in HBM (built by the repack/generator kernels): the rows of a
-// matrix are taken in groups of 64 (one row per lane), and within a group the
-// 16-byte nibble payloads are stored block-major:
-//   nib[grp][b][l]        uint4   block b (32 weights) of row 64*grp + l
-//   sc [grp][b/4][l][b%4] uint8   its E8M0 exponent (4 blocks per dword)
-// where grp = matrix * (R/64) + row/64 over all experts of a tensor.  A wave
-// reading block b of a row group loads 64 x 16 B = 1 KiB contiguous, and one
-// dword per lane carries the exponents of 4 blocks.  The nibble bytes keep
-// ggml's order (byte j = element j | element j+16 << 4), so activations are
-// stored as fp16 pairs (q_j, q_{j+16}) to meet them.
+// Weight layout in HBM (written by the repack/generator kernels, see
+// kernels_weights.h): rows in tiles of 16, the reduction dim in quads of
+// 4 blocks (128 weights); for every (tile, quad) the 64 lanes of a wave read
+// one contiguous KiB:
+//   nib[tile][q][l]      uint4  the 16 nibble bytes of block 4q + l/16 of
+//                               row 16*tile + l%16 (ggml's bytes, unchanged)
+//   sc [tile][q/4][l]    u32    byte q%4: that block's E8M0 exponent
+// which is exactly the A-operand lane layout of the 16x16x128 MFMA: lane
+// r + 16g holds row r, K-block g, nibble e at K offset e.  A ggml byte j holds
+// element j (low nibble) and j+16 (high), so K offset e of a block carries
+// element sigma(e) = e/2 + 16*(e%2); the activations are laid out to match.
 //
-// Work mapping: lane <-> row, so a row's dot product never crosses lanes.
-// The reduction dimension K (in blocks) is split over the waves of a
-// workgroup; each wave streams its K-chunk of 64 rows with the next 4 blocks'
-// loads in flight while it computes the current 4, against activations
-// staged in LDS (read by all lanes at one address: a broadcast).  Partials
-// are summed over waves in wave order through LDS, so results do not depend
-// on timing.
+// Activations.  ggml quantizes them to Q8_0: per 32-block an fp16 scale d
+// and int8 codes q in [-127, 127].  Each code is split into two exact e4m3
+// digits, hi = q >> 4 in [-8, 7] and lo = q & 15 in [0, 15] (q = 16*hi + lo),
+// and the B operand is block-diagonal: column n = 8*token + 4*part + g of the
+// MFMA holds part (0 = hi, 1 = lo) of block g of the quad, for two tokens.
+// The B scale of a hi column is 2^4, of a lo column 2^0, so every output
+// column is 2^(e_w - 127) times an exact integer block sum (all products and
+// partial sums are small integers in f32), i.e. ggml's per-block integer dot
+// times the weight scale.  The activation scale d of each (token, block) is
+// then applied in f32 by the lane that holds that column, and the 8 columns
+// of a token are added in a fixed order at the end: ggml-cpu's MXFP4 x Q8_0
+// arithmetic with another (fixed) f32 summation order.
 //
-// Arithmetic (ggml-cpu's MXFP4 x Q8_0): per block, isum = sum of e2m1 code
-// values x int8 activations, exact (v_cvt_scalef32_pk_f16_fp4 -> fp16 pairs,
-// v_dot2_f32_f16 -> f32, all terms small integers / halves); the block adds
-// fp16(d_x) * 2^(e-127) * isum/2 to an f32 accumulator.
+// B-operand lane layout (probed on the device): lane n + 16*gb holds column
+// n; its bytes 0-15 are K offsets 16*gb + [0, 16), bytes 16-31 are K offsets
+// 64 + 16*gb + [0, 16).  So block g's 32 bytes go to lanes gb = 2*(g%2) + h
+// (h = half), in bytes 16*(g/2) + [0, 16).
+//
+// Staged activations ("xs" format, LDS and the h buffers): per block 16
+// dwords, hi[8] then lo[8], each the 32 e4m3 digits in MFMA K order, plus
+// the block's fp16 scale d widened to f32 in a separate array.
 #pragma once
 
 #include "device_common.h"
 
-#define MOE_RG 64         // rows per row group (= lanes per wave)
-#define MOE_GU_WAVES 8    // waves per gate/up workgroup (K split 8 ways)
-#define MOE_DN_WAVES 4    // waves per down workgroup (K split 4 ways)
+#define MOE_TILE 16     // rows per MFMA tile
+#define MOE_UNIT 32     // rows per h unit (one Q8_0 block of the SwiGLU output)
+#define MOE_XSW 16      // dwords per staged block
+#define MOE_GRP_WAVES 4 // waves per grouped-kernel workgroup (K split 4 ways)
 
-// ---------------------------------------------------------------------------
-// Split of KQ = KB/4 block groups over NW waves: wave w owns [q0, q1).
-__device__ __forceinline__ void wave_groups(int KQ, int NW, int w, int &q0, int &q1) {
-  q0 = (int)(((long)KQ * w) / NW);
-  q1 = (int)(((long)KQ * (w + 1)) / NW);
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef int i32x8_t __attribute__((ext_vector_type(8)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+__host__ __device__ __forceinline__ int moe_nq4(int NQ) { return (NQ + 3) >> 2; }
+
+// Split of n items over c parts: part i owns [lo, hi).
+__host__ __device__ __forceinline__ void split_range(int n, int c, int i, int &lo, int &hi) {
+  lo = (int)(((long)n * i) / c);
+  hi = (int)(((long)n * (i + 1)) / c);
 }
 
-// Largest number of blocks any wave owns (host and device agree on it).
-__host__ __device__ __forceinline__ int max_wave_blocks(int KB, int NW) {
-  const int KQ = KB / 4;
-  return 4 * ((KQ + NW - 1) / NW);
+// ---------------------------------------------------------------------------
+// e4m3 digits
+
+// Four small integers (exact in e4m3) -> one dword of e4m3 bytes, a in byte 0.
+__device__ __forceinline__ uint32_t pack_e4m3x4(float a, float b, float c, float d) {
+  int w = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
+  w = __builtin_amdgcn_cvt_pk_fp8_f32(c, d, w, true);
+  return (uint32_t)w;
 }
 
+__device__ __forceinline__ float q_hi(float q) { return (float)(((int)q) >> 4); }
+__device__ __forceinline__ float q_lo(float q) { return (float)(((int)q) & 15); }
+
 // ---------------------------------------------------------------------------
-// Q8_0 of nb blocks of one f32 row into LDS, ggml's x86 rounding:
-// amax per block, d = fp16(amax / 127), q = rint(x * (127 / amax)).
-// Two lanes per block: lane half 0 takes elements 0-7 and 16-23, half 1
-// takes 8-15 and 24-31, so each lane forms its 8 (q_j, q_{j+16}) pairs.
-// q_s: [nb][16] packed fp16 pairs; d_s: [nb] fp16(d) as f32.
-__device__ __forceinline__ void stage_quantize(const float *__restrict__ xrow, int nb, uint32_t *q_s,
-                                               float *d_s, int lane) {
-  const int half = lane & 1;
-  for (int bb = lane >> 1; bb < nb; bb += 32) {
-    const float4 *xb = reinterpret_cast<const float4 *>(xrow + (size_t)bb * MOE_QK + 8 * half);
+// Staging into LDS.  Two lanes per block: lane half h takes elements
+// 8h..8h+7 and 16+8h..16+8h+7, which are exactly the MFMA K offsets
+// 16h..16h+15 of the block (offset 2i -> element 8h+i, 2i+1 -> 16+8h+i).
+
+// Q8_0 of nb blocks of one f32 row (ggml's x86 rounding: d = fp16(amax/127),
+// q = rint(x * 127/amax)) into the staged format.
+__device__ __forceinline__ void stage_quant(const float *__restrict__ x, int nb, uint32_t *xs, float *dy, int lane) {
+  const int h = lane & 1;
+  for (int b = lane >> 1; b < nb; b += 32) {
+    const float4 *xb = reinterpret_cast<const float4 *>(x + (size_t)b * MOE_QK + 8 * h);
     const float4 a0 = xb[0], a1 = xb[1], c0 = xb[4], c1 = xb[5];
     const float lo[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
     const float hi[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
@@ -62,148 +88,293 @@ __device__ __forceinline__ void stage_quantize(const float *__restrict__ xrow, i
 #pragma unroll
     for (int i = 0; i < 8; i++) amax = fmaxf(amax, fmaxf(fabsf(lo[i]), fabsf(hi[i])));
     amax = fmaxf(amax, dpp_f<0xB1>(amax));  // partner lane (lane ^ 1) holds the other half
-    uint32_t pk[8];
+    uint32_t wh[4], wl[4];
 #pragma unroll
-    for (int i = 0; i < 8; i++) pk[i] = pack_f16x2(q8_code(lo[i], amax), q8_code(hi[i], amax));
-    uint4 *dst = reinterpret_cast<uint4 *>(q_s + (size_t)bb * 16 + 8 * half);
-    dst[0] = make_uint4(pk[0], pk[1], pk[2], pk[3]);
-    dst[1] = make_uint4(pk[4], pk[5], pk[6], pk[7]);
-    if (!half) d_s[bb] = (float)q8_scale_f16(amax);
+    for (int i = 0; i < 4; i++) {
+      const float q0 = q8_code(lo[2 * i], amax), q1 = q8_code(hi[2 * i], amax);
+      const float q2 = q8_code(lo[2 * i + 1], amax), q3 = q8_code(hi[2 * i + 1], amax);
+      wh[i] = pack_e4m3x4(q_hi(q0), q_hi(q1), q_hi(q2), q_hi(q3));
+      wl[i] = pack_e4m3x4(q_lo(q0), q_lo(q1), q_lo(q2), q_lo(q3));
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(xs + (size_t)b * MOE_XSW);
+    dst[h] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+    dst[2 + h] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+    if (!h) dy[b] = (float)q8_scale_f16(amax);
   }
 }
 
-// Copy nb pre-quantized blocks (global [nb][16] pairs + [nb] scales) into LDS.
-__device__ __forceinline__ void stage_copy(const uint32_t *__restrict__ q, const float *__restrict__ d, int nb,
-                                           uint32_t *q_s, float *d_s, int lane) {
-  for (int i = lane; i < nb * 4; i += 64)
-    reinterpret_cast<uint4 *>(q_s)[i] = reinterpret_cast<const uint4 *>(q)[i];
-  for (int i = lane; i < nb; i += 64) d_s[i] = d[i];
+// Copy nb staged blocks from global memory into LDS.  COHERENT: the source
+// was written by another workgroup of the same launch, so the loads are
+// agent-scope (they bypass the XCD's L2); otherwise plain loads.
+template <bool COHERENT>
+__device__ __forceinline__ void stage_copy(const uint32_t *__restrict__ src, const float *__restrict__ sd, int nb,
+                                           uint32_t *xs, float *dy, int lane) {
+  for (int i = lane; i < nb * 4; i += 64) {
+    uint4 v;
+    if (COHERENT) {
+      const uint32_t *p = src + (size_t)i * 4;
+      v.x = __hip_atomic_load(p + 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v.y = __hip_atomic_load(p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v.z = __hip_atomic_load(p + 2, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      v.w = __hip_atomic_load(p + 3, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      v = reinterpret_cast<const uint4 *>(src)[i];
+    }
+    reinterpret_cast<uint4 *>(xs)[i] = v;
+  }
+  for (int i = lane; i < nb; i += 64)
+    dy[i] = COHERENT ? __hip_atomic_load(sd + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) : sd[i];
 }
 
-// Zero nb staged blocks (token slots of a partial batch).
-__device__ __forceinline__ void stage_zero(int nb, uint32_t *q_s, float *d_s, int lane) {
-  for (int i = lane; i < nb * 4; i += 64) reinterpret_cast<uint4 *>(q_s)[i] = make_uint4(0u, 0u, 0u, 0u);
-  for (int i = lane; i < nb; i += 64) d_s[i] = 0.0f;
+__device__ __forceinline__ void stage_zero(int nb, uint32_t *xs, float *dy, int lane) {
+  for (int i = lane; i < nb * 4; i += 64) reinterpret_cast<uint4 *>(xs)[i] = make_uint4(0u, 0u, 0u, 0u);
+  for (int i = lane; i < nb; i += 64) dy[i] = 0.0f;
 }
 
 // ---------------------------------------------------------------------------
-// Loads of one group of 4 blocks for NM matrices (16 B payload per block per
-// lane, one exponent dword per lane).  Weights are read once per call, so the
-// loads are nontemporal (they bypass the caches' normal allocation).
-typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
-
-template <int NM>
-struct wgroup {
-  u32x4_t w[NM][4];
-  uint32_t e[NM];
+// Per-lane B-operand configuration for one token pair.
+struct bsel {
+  int off_lo, step_lo;  // dword offset (in xs) of the B bytes 0-15 and its step per quad (0: a zero area)
+  int off_hi, step_hi;  // same for bytes 16-31
+  int dy_off;           // offset of this column's d (in dy) at quad 0; < 0: no token
+  int sb;               // B scale: 2^4 (hi part) or 2^0 (lo part), E8M0
 };
 
-template <int NM>
-__device__ __forceinline__ void load_group(wgroup<NM> &g, const uint4 *const (&nib)[NM],
-                                           const uint32_t *const (&sc)[NM], int q, int lane) {
-#pragma unroll
-  for (int m = 0; m < NM; m++) {
-#pragma unroll
-    for (int i = 0; i < 4; i++)
-      g.w[m][i] = __builtin_nontemporal_load(
-          reinterpret_cast<const u32x4_t *>(nib[m] + (size_t)(4 * q + i) * MOE_RG + lane));
-    g.e[m] = __builtin_nontemporal_load(sc[m] + (size_t)q * MOE_RG + lane);
-  }
+// xs_tok[t] / dy_tok[t]: staged rows of the two tokens (quad 0 of the
+// lane's K range); tv[t]: token present.  zero_off: a 16-byte zero area.
+__device__ __forceinline__ bsel make_bsel(int lane, int xs_tok0, int xs_tok1, int dy_tok0, int dy_tok1, bool tv0,
+                                          bool tv1, int zero_off) {
+  const int n = lane & 15, gb = lane >> 4;
+  const int tp = n >> 3, part = (n >> 2) & 1, g = n & 3;
+  const bool tv = tp ? tv1 : tv0;
+  const bool holds = tv && ((gb >> 1) == (g & 1));
+  const int off = (tp ? xs_tok1 : xs_tok0) + g * MOE_XSW + part * 8 + (gb & 1) * 4;
+  bsel s;
+  const bool upper = g >= 2;
+  s.off_lo = holds && !upper ? off : zero_off;
+  s.step_lo = holds && !upper ? 4 * MOE_XSW : 0;
+  s.off_hi = holds && upper ? off : zero_off;
+  s.step_hi = holds && upper ? 4 * MOE_XSW : 0;
+  s.dy_off = tv ? (tp ? dy_tok1 : dy_tok0) + g : -1;
+  s.sb = part ? 127 : 131;
+  return s;
 }
 
-// acc[m][t] += the 4 blocks of group g (local group index lq) against the
-// NT staged tokens.
-template <int NM, int NT>
-__device__ __forceinline__ void dot_group(const wgroup<NM> &g, int lq, const uint32_t *q_s, const float *d_s,
-                                          int NBW, float (&acc)[NM][NT]) {
-#pragma unroll
-  for (int i = 0; i < 4; i++) {
-    const int lb = 4 * lq + i;
-    float dot[NM][NT];
-#pragma unroll
-    for (int m = 0; m < NM; m++)
-#pragma unroll
-      for (int t = 0; t < NT; t++) dot[m][t] = 0.0f;
-#pragma unroll
-    for (int dw = 0; dw < 4; dw++) {
-      f16x2_t w[NM][4];
-#pragma unroll
-      for (int m = 0; m < NM; m++) {
-        const uint32_t v = g.w[m][i][dw];
-        w[m][0] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 0);
-        w[m][1] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 1);
-        w[m][2] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 2);
-        w[m][3] = __builtin_amdgcn_cvt_scalef32_pk_f16_fp4(v, 1.0f, 3);
-      }
-#pragma unroll
-      for (int t = 0; t < NT; t++) {
-        const uint4 a = reinterpret_cast<const uint4 *>(q_s + (size_t)(t * NBW + lb) * 16)[dw];
-#pragma unroll
-        for (int m = 0; m < NM; m++) {
-          float s = dot[m][t];
-          s = __builtin_amdgcn_fdot2(w[m][0], __builtin_bit_cast(f16x2_t, a.x), s, false);
-          s = __builtin_amdgcn_fdot2(w[m][1], __builtin_bit_cast(f16x2_t, a.y), s, false);
-          s = __builtin_amdgcn_fdot2(w[m][2], __builtin_bit_cast(f16x2_t, a.z), s, false);
-          s = __builtin_amdgcn_fdot2(w[m][3], __builtin_bit_cast(f16x2_t, a.w), s, false);
-          dot[m][t] = s;
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      const float xd = d_s[t * NBW + lb];
-#pragma unroll
-      for (int m = 0; m < NM; m++) {
-        const uint32_t e = (g.e[m] >> (8 * i)) & 0xFFu;
-        acc[m][t] = fmaf(scale_e8m0(xd, e), dot[m][t], acc[m][t]);
-      }
-    }
-  }
+__device__ __forceinline__ i32x8_t load_b(const bsel &s, const uint32_t *xs, int ql) {
+  const u32x4_t lo = *reinterpret_cast<const u32x4_t *>(xs + s.off_lo + ql * s.step_lo);
+  const u32x4_t hi = *reinterpret_cast<const u32x4_t *>(xs + s.off_hi + ql * s.step_hi);
+  i32x8_t b;
+  b[0] = (int)lo.x; b[1] = (int)lo.y; b[2] = (int)lo.z; b[3] = (int)lo.w;
+  b[4] = (int)hi.x; b[5] = (int)hi.y; b[6] = (int)hi.z; b[7] = (int)hi.w;
+  return b;
 }
 
-// One wave: NM matrices (same row group, same K) x NT staged tokens over nq
-// groups of 4 blocks.  nib[m] / sc[m] point at the wave's first block of the
-// row group; activation block lb of token t is at q_s + (t*NBW + lb)*16 and
-// d_s + t*NBW + lb.  A ring of D load buffers keeps D-1 groups in flight
-// while one is computed; the loads are always issued (past the end they
-// re-read the last group, an L2 hit), so the wait before each group's math
-// covers only that group's own loads.  ring_prime() issues groups 0..D-2 and
-// is called by the kernel before it stages the activations, so the first
-// weight loads overlap the staging.
-template <int NM, int D>
-__device__ __forceinline__ void ring_prime(wgroup<NM> (&buf)[D], const uint4 *const (&nib)[NM],
-                                           const uint32_t *const (&sc)[NM], int nq, int lane) {
-  if (nq <= 0) return;
-#pragma unroll
-  for (int d = 0; d < D - 1; d++) load_group<NM>(buf[d], nib, sc, d < nq ? d : nq - 1, lane);
+__device__ __forceinline__ float load_dy(const bsel &s, const float *dy, int ql) {
+  return s.dy_off >= 0 ? dy[s.dy_off + 4 * ql] : 0.0f;
 }
 
-template <int NM, int NT, int D>
-__device__ __forceinline__ void rows_dot(wgroup<NM> (&buf)[D], const uint4 *const (&nib)[NM],
-                                         const uint32_t *const (&sc)[NM], int nq, const uint32_t *q_s,
-                                         const float *d_s, int NBW, int lane, float (&acc)[NM][NT]) {
-#pragma unroll
-  for (int m = 0; m < NM; m++)
-#pragma unroll
-    for (int t = 0; t < NT; t++) acc[m][t] = 0.0f;
-  if (nq <= 0) return;
-  for (int q0 = 0;; q0 += D) {
-#pragma unroll
-    for (int d = 0; d < D; d++) {
-      const int q = q0 + d, qn = q + D - 1;
-      load_group<NM>(buf[(d + D - 1) % D], nib, sc, qn < nq ? qn : nq - 1, lane);
-      __builtin_amdgcn_sched_barrier(0);  // keep the prefetch ahead of the math
-      dot_group<NM, NT>(buf[d], q, q_s, d_s, NBW, acc);
-      if (q + 1 >= nq) return;
-    }
-  }
+__device__ __forceinline__ f32x4_t mfma_blk(const u32x4_t w, const i32x8_t b, int sa, int sb) {
+  const i32x8_t a = {(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+  const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 4, 0, 0, sa, 0, sb);
+}
+
+// Sum of the 8 columns of each token, left in the lanes of columns 0 and 8:
+// ((c0 + c1) + (c2 + c3)) + ((c4 + c5) + (c6 + c7)).
+__device__ __forceinline__ float col8_sum(float v) {
+  v += dpp_f<0xB1>(v);  // lane ^ 1
+  v += dpp_f<0x4E>(v);  // lane ^ 2
+  v += __shfl_xor(v, 4);
+  return v;
 }
 
 // ---------------------------------------------------------------------------
-// Which expert matrix and which rows workgroup column y works on.
+// A wave's K loop: NW weight streams ((matrix, tile) pairs), quads [q0, q1)
+// with q0 % 4 == 0, against NP staged token pairs.  The loads run 3 quads
+// ahead of the math (a ring of 4, so quad q sits in slot (q - q0) % 4, a
+// compile-time index); the exponent dwords (4 quads each) are loaded once per
+// group of 4 quads, one group ahead, and the MFMA's op_sel picks the quad's
+// byte.  Past the end the ring re-reads the last quad (an L2 hit), so every
+// wait covers only the quad about to be used.
+template <int NW>
+struct wquad {
+  u32x4_t w[NW];
+};
+
+// One weight stream: a (matrix, tile) pair as two buffer resources (base in
+// SGPRs, bounds-checked: a read past the tile returns 0), its nibble quads and
+// its exponent dwords.
+struct wstream {
+  __amdgpu_buffer_rsrc_t nib, sc;
+};
+
+#define MOE_RSRC_FLAGS 0x00020000  // raw buffer, 32-bit dwords, no swizzle
+#define MOE_CPOL_NT 2              // non-temporal loads: weights are read once per call
+
+__device__ __forceinline__ wstream make_wstream(const uint4 *nib, const uint32_t *sc, size_t tile, int NQ, int NQ4) {
+  wstream w;
+  w.nib = __builtin_amdgcn_make_buffer_rsrc((void *)(nib + tile * NQ * 64), 0, NQ * 1024, MOE_RSRC_FLAGS);
+  w.sc = __builtin_amdgcn_make_buffer_rsrc((void *)(sc + tile * NQ4 * 64), 0, NQ4 * 256, MOE_RSRC_FLAGS);
+  return w;
+}
+
+template <int NW>
+__device__ __forceinline__ void load_wquad(wquad<NW> &b, const wstream (&ws)[NW], int q, int lane) {
+#pragma unroll
+  for (int i = 0; i < NW; i++)
+    b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(ws[i].nib, lane * 16, q * 1024, MOE_CPOL_NT);
+}
+
+template <int NW>
+__device__ __forceinline__ void load_scales(uint32_t (&sc)[NW], const wstream (&ws)[NW], int g, int lane) {
+#pragma unroll
+  for (int i = 0; i < NW; i++) sc[i] = __builtin_amdgcn_raw_buffer_load_b32(ws[i].sc, lane * 4, g * 256, 0);
+}
+
+template <int SEL>
+__device__ __forceinline__ f32x4_t mfma_blk(const u32x4_t w, const i32x8_t b, uint32_t sa, int sb) {
+  const i32x8_t a = {(int)w.x, (int)w.y, (int)w.z, (int)w.w, 0, 0, 0, 0};
+  const f32x4_t z = {0.0f, 0.0f, 0.0f, 0.0f};
+  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a, b, z, 4, 0, SEL, (int)sa, 0, sb);
+}
+
+// acc[p][i] += quad ql (local) of stream i against token pair p; SEL = q % 4.
+template <int SEL, int NW, int NP>
+__device__ __forceinline__ void quad_mma(const wquad<NW> &b, const uint32_t (&sc)[NW], int ql, const bsel (&bs)[NP],
+                                         const uint32_t *xs, const float *dy, f32x4_t (&acc)[NP][NW]) {
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    const i32x8_t bv = load_b(bs[p], xs, ql);
+    const float d = load_dy(bs[p], dy, ql);
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+      const f32x4_t r = mfma_blk<SEL>(b.w[i], bv, sc[i], bs[p].sb);
+      acc[p][i] = acc[p][i] + d * r;
+    }
+  }
+  // pin this quad's math here: without it the compiler sinks the (pure)
+  // MFMAs below the following quads' loads, keeping every quad's weights live
+#pragma unroll
+  for (int p = 0; p < NP; p++)
+#pragma unroll
+    for (int i = 0; i < NW; i++) asm volatile("" : "+v"(acc[p][i]));
+}
+
+template <int NW>
+struct kring {
+  wquad<NW> q[4];
+  uint32_t sc[NW];
+};
+
+// Issue the first 3 quads and the first exponent group (call before staging
+// the activations, so the weight loads overlap it).
+template <int NW>
+__device__ __forceinline__ void kloop_prime(kring<NW> &r, const wstream (&ws)[NW], int q0, int q1, int lane) {
+  if (q1 <= q0) return;
+#pragma unroll
+  for (int d = 0; d < 3; d++) load_wquad<NW>(r.q[d], ws, q0 + d < q1 ? q0 + d : q1 - 1, lane);
+  load_scales<NW>(r.sc, ws, q0 >> 2, lane);
+}
+
+// K loop over quads [q0, q1).  The main loop covers whole groups of 4 quads
+// with no exit inside, and each quad's loads and math are pinned in order
+// (quad_mma's asm pins, the memory fence below), so the 4 ring slots keep
+// their registers across iterations: no copies at the back edge, which
+// would wait for every load in flight.  The last partial group is a
+// guarded tail.
+template <int NW, int NP>
+__device__ __forceinline__ void kloop(kring<NW> &r, const wstream (&ws)[NW], int q0, int q1, const bsel (&bs)[NP],
+                                          const uint32_t *xs, const float *dy, int lane, f32x4_t (&acc)[NP][NW]) {
+#pragma unroll
+  for (int p = 0; p < NP; p++)
+#pragma unroll
+    for (int i = 0; i < NW; i++) acc[p][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  if (q1 <= q0) return;
+  const int glast = (q1 - 1) >> 2;
+  uint32_t scn[NW];
+#define MOE_KSTEP(J)                                                    \
+  {                                                                     \
+    const int q = qb + J, qn = q + 3;                                   \
+    load_wquad<NW>(r.q[(J + 3) & 3], ws, qn < q1 ? qn : q1 - 1, lane);  \
+    asm volatile("" ::: "memory");     /* no hoisting of later loads */ \
+    __builtin_amdgcn_sched_barrier(0); /* keep the prefetch ahead */    \
+    quad_mma<J, NW, NP>(r.q[J], r.sc, q - q0, bs, xs, dy, acc);         \
+  }
+  int qb = q0;
+  for (; qb + 4 <= q1; qb += 4) {
+    const int gn = (qb >> 2) + 1;
+    load_scales<NW>(scn, ws, gn < glast ? gn : glast, lane);
+    MOE_KSTEP(0)
+    MOE_KSTEP(1)
+    MOE_KSTEP(2)
+    MOE_KSTEP(3)
+#pragma unroll
+    for (int i = 0; i < NW; i++) r.sc[i] = scn[i];
+  }
+  // tail: 1-3 quads of the last group (their exponents are in r.sc)
+  if (qb < q1) MOE_KSTEP(0)
+  if (qb + 1 < q1) MOE_KSTEP(1)
+  if (qb + 2 < q1) MOE_KSTEP(2)
+#undef MOE_KSTEP
+}
+
+// ---------------------------------------------------------------------------
+// SwiGLU + Q8_0 of one 32-row h unit held by 32 consecutive lanes (lane j of
+// the half = row j; `base` = the half's first lane), written in the staged
+// format: 16 dwords at hs, scale at *hd.  All 64 lanes of the wave call it.
+__device__ __forceinline__ float swiglu(float g, float up, float clamp) {
+  if (clamp > 1e-6f) {  // deepseek4 order: up symmetric, gate one-sided, before SiLU
+    up = fmaxf(fminf(up, clamp), -clamp);
+    g = fminf(g, clamp);
+  }
+  return __fmul_rn(__fdiv_rn(g, 1.0f + expf(-g)), up);
+}
+
+// amax over each 32-lane half of the wave
+__device__ __forceinline__ float half_amax(float v) {
+  v = fmaxf(v, dpp_f<0xB1>(v));
+  v = fmaxf(v, dpp_f<0x4E>(v));
+  v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+  return fmaxf(v, __shfl_xor(v, 16));
+}
+
+// Returns the dword lane j (< 16 of its half) writes: dword j of the staged
+// block (hi[8] then lo[8]); the codes come from lanes of the same half.
+// Dword w = 4h + i of a part holds elements 8h+2i, 16+8h+2i, 8h+2i+1,
+// 16+8h+2i+1 (bytes 0..3).
+__device__ __forceinline__ uint32_t h_unit_dword(float q, int lane) {
+  const int base = lane & 32, j = lane & 31;
+  const int part = (j >> 3) & 1, w = j & 7, hh = w >> 2, i = w & 3;
+  const int e0 = base + 8 * hh + 2 * i, e1 = base + 16 + 8 * hh + 2 * i;
+  const int src[4] = {e0, e1, e0 + 1, e1 + 1};
+  const float qh = q_hi(q), ql = q_lo(q);
+  float v[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    const float a = __shfl(qh, src[k]), b = __shfl(ql, src[k]);
+    v[k] = part ? b : a;
+  }
+  return pack_e4m3x4(v[0], v[1], v[2], v[3]);
+}
+
+// Q8_0 of the 32-row h unit in each half of the wave (lane j of a half =
+// row j), written to hs (16 dwords) / *hd when `store` (wave-uniform per
+// half is not required: lanes store only their own dword).
+__device__ __forceinline__ void h_unit_store(float h, bool store, uint32_t *hs, float *hd, int lane) {
+  const float am = half_amax(fabsf(h));
+  const float q = q8_code(h, am);
+  const uint32_t dw = h_unit_dword(q, lane);
+  const int j = lane & 31;
+  if (store && j < 16) hs[j] = dw;
+  if (store && j == 0) *hd = (float)q8_scale_f16(am);
+}
+
+// ---------------------------------------------------------------------------
+// Which expert matrix and which h rows workgroup column y works on.
 //   decode (T == 1): y = slot s; s < k -> expert ids[s], s == k -> shared
-//     expert (matrix E); one token; h/y row index = s.
-//   grouped: y < act[0] -> expert act[1+y], h/y rows offsets[e]..offsets[e+1]
+//     expert (matrix E); one token; h row s.
+//   grouped: y < act[0] -> expert act[1+y], h rows offsets[e]..offsets[e+1]
 //     (token of row r = perm[r] / k); last y when `shared` -> the shared
 //     expert, rows P..P+T-1 (token of row P+i = i).
 struct unit_t {
@@ -244,422 +415,278 @@ __device__ __forceinline__ unit_t unit_of(int y, int ny, bool grouped, const int
   return u;
 }
 
-__device__ __forceinline__ int token_of(bool grouped, const unit_t &u, int hrow, const int32_t *__restrict__ perm,
-                                        int k, int P) {
-  if (!grouped) return 0;
+__device__ __forceinline__ int token_of(const unit_t &u, int hrow, const int32_t *__restrict__ perm, int k, int P) {
   return u.shared ? hrow - P : perm[hrow] / k;
 }
 
 // ---------------------------------------------------------------------------
-// gate/up -> clamp -> SwiGLU -> Q8_0(h).  grid (F/64, ny), MOE_GU_WAVES waves.
-// Dynamic LDS: MOE_GU_WAVES * NT * NBW * 68 B (activations) + the partials.
-template <int NT>
-__global__ __launch_bounds__(64 * MOE_GU_WAVES) __attribute__((amdgpu_waves_per_eu(NT == 1 ? 4 : 2))) void k_gate_up(
+// K split of the workgroup kernels: wave w of NW owns the 4-quad groups
+// [g0, g1) of ceil(NQ/4), i.e. quads [4*g0, min(4*g1, NQ)).
+__host__ __device__ __forceinline__ void wave_quads(int NQ, int NW, int w, int &q0, int &q1) {
+  int g0, g1;
+  split_range(moe_nq4(NQ), NW, w, g0, g1);
+  q0 = 4 * g0;
+  q1 = 4 * g1 < NQ ? 4 * g1 : NQ;
+  if (q1 < q0) q1 = q0;
+}
+// Largest number of staged blocks any wave holds.
+__host__ __device__ __forceinline__ int wave_blocks(int NQ, int NW) {
+  return 16 * ((moe_nq4(NQ) + NW - 1) / NW);
+}
+
+// gate/up -> clamp -> SwiGLU -> Q8_0(h).  One workgroup of 4 waves per
+// (32-row unit of F, expert column y).  The waves split the reduction dim;
+// each stages its part of the activations of a batch of up to 2*NP tokens,
+// streams its quads of the unit's 2 tiles of gate and up once per batch, and
+// the partial sums meet in LDS in wave order; then one wave per 2 tokens
+// applies clamp + SwiGLU and quantizes the unit's 32 h values (one Q8_0
+// block per token).  Decode (grouped == 0) is the same kernel with column
+// y = slot and one token.  grid (F/32, ny), 256 threads.
+// LDS: per wave [zero 4][xs 2NP*NBW*16][dy 2NP*NBW] dwords, reused for the
+// partials [wave][4 streams][2NP][16] after the K loops.
+// NP == 1 (decode and small batches) is held to 3 waves per SIMD, so a
+// V3 decode's 576 workgroups are resident at once (3 per CU).
+template <int NP>
+__global__ __launch_bounds__(64 * MOE_GRP_WAVES) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 3 : (NP == 2 ? 2 : 1))))
+void k_gate_up(
     const uint4 *__restrict__ nib_g, const uint4 *__restrict__ nib_u, const uint32_t *__restrict__ sc_g,
-    const uint32_t *__restrict__ sc_u, const float *__restrict__ x, int grouped,
-    const int32_t *__restrict__ ids, const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm,
-    const int32_t *__restrict__ act, int k, int E, int shared, int T, int F, int H, float clamp,
-    uint32_t *__restrict__ hq, float *__restrict__ hd, float *__restrict__ htap) {
+    const uint32_t *__restrict__ sc_u, const float *__restrict__ x, int grouped, const int32_t *__restrict__ ids,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm, const int32_t *__restrict__ act, int k,
+    int E, int shared, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
+    float *__restrict__ htap) {
   extern __shared__ __align__(16) uint32_t lds[];
-  const int KB = H / MOE_QK, KQ = KB / 4, NBW = max_wave_blocks(KB, MOE_GU_WAVES);
+  constexpr int NTOK = 2 * NP;
+  const int NQ = H / 128, NQ4 = moe_nq4(NQ), U = F / MOE_UNIT, tiles = F / MOE_TILE;
+  const int NBW = wave_blocks(NQ, MOE_GRP_WAVES);
+  const int wave_words = 4 + NTOK * NBW * (MOE_XSW + 1);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = T * k;
-  const unit_t u = unit_of(blockIdx.y, gridDim.y, grouped, ids, offsets, act, k, E, shared, P, T);
-  if (!u.valid && grouped) return;
+  const unit_t un = unit_of(blockIdx.y, gridDim.y, grouped, ids, offsets, act, k, E, shared, P, T);
+  if (grouped && !un.valid) return;
+  const int u = blockIdx.x;
   int q0, q1;
-  wave_groups(KQ, MOE_GU_WAVES, wave, q0, q1);
-  const int nbw = 4 * (q1 - q0);
-  uint32_t *q_s = lds + (size_t)wave * NT * NBW * 16;
-  float *d_s = reinterpret_cast<float *>(lds + (size_t)MOE_GU_WAVES * NT * NBW * 16) + (size_t)wave * NT * NBW;
-  float *red = reinterpret_cast<float *>(lds + (size_t)MOE_GU_WAVES * NT * NBW * 17);  // [waves][2][NT][64]
-
-  const int G = F / MOE_RG;
-  const size_t grp = (size_t)u.mat * G + blockIdx.x;
-  const uint4 *const nibs[2] = {nib_g + grp * KB * MOE_RG + (size_t)4 * q0 * MOE_RG,
-                                nib_u + grp * KB * MOE_RG + (size_t)4 * q0 * MOE_RG};
-  const uint32_t *const scs[2] = {sc_g + grp * KQ * MOE_RG + (size_t)q0 * MOE_RG,
-                                  sc_u + grp * KQ * MOE_RG + (size_t)q0 * MOE_RG};
-
-  const int nq = q1 - q0;
-  for (int i0 = 0; i0 < u.nrows; i0 += NT) {
-    const int nt = u.nrows - i0 < NT ? u.nrows - i0 : NT;
-    wgroup<2> ring[2];
-    ring_prime<2, 2>(ring, nibs, scs, nq, lane);
-    // stage this wave's K-chunk of the batch's activations
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      if (t < nt && u.valid) {
-        const int tok = token_of(grouped, u, u.row0 + i0 + t, perm, k, P);
-        stage_quantize(x + (size_t)tok * H + (size_t)4 * q0 * MOE_QK, nbw, q_s + (size_t)t * NBW * 16,
-                       d_s + (size_t)t * NBW, lane);
-      } else {
-        stage_zero(nbw, q_s + (size_t)t * NBW * 16, d_s + (size_t)t * NBW, lane);
-      }
+  wave_quads(NQ, MOE_GRP_WAVES, wave, q0, q1);
+  const int nb = 4 * (q1 - q0);
+  uint32_t *xs = lds + (size_t)wave * wave_words;
+  float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)NTOK * NBW * MOE_XSW);
+  float *red = reinterpret_cast<float *>(lds);  // [wave][4 streams][NTOK][16], after the K loops
+  const size_t t0 = (size_t)un.mat * tiles + 2 * u;
+  const wstream ws[4] = {make_wstream(nib_g, sc_g, t0, NQ, NQ4), make_wstream(nib_g, sc_g, t0 + 1, NQ, NQ4),
+                         make_wstream(nib_u, sc_u, t0, NQ, NQ4), make_wstream(nib_u, sc_u, t0 + 1, NQ, NQ4)};
+  for (int i0 = 0; i0 < un.nrows; i0 += NTOK) {
+    const int nt = un.nrows - i0 < NTOK ? un.nrows - i0 : NTOK;
+    kring<4> ring;
+    kloop_prime<4>(ring, ws, q0, q1, lane);
+    if (lane < 4) xs[lane] = 0u;
+    for (int t = 0; t < nt; t++) {
+      const int tok = grouped ? token_of(un, un.row0 + i0 + t, perm, k, P) : 0;
+      stage_quant(x + (size_t)tok * H + (size_t)q0 * 128, nb, xs + 4 + (size_t)t * NBW * MOE_XSW,
+                  dy + (size_t)t * NBW, lane);
     }
-    float acc[2][NT];
-    rows_dot<2, NT, 2>(ring, nibs, scs, nq, q_s, d_s, NBW, lane, acc);
-#pragma unroll
-    for (int m = 0; m < 2; m++)
-#pragma unroll
-      for (int t = 0; t < NT; t++) red[((wave * 2 + m) * NT + t) * MOE_RG + lane] = acc[m][t];
     __syncthreads();
-    // epilogue: wave t finishes token t of the batch
-    if (wave < nt) {
-      const int t = wave;
-      float g = 0.0f, up = 0.0f;
-      for (int w = 0; w < MOE_GU_WAVES; w++) {
-        g += red[((w * 2 + 0) * NT + t) * MOE_RG + lane];
-        up += red[((w * 2 + 1) * NT + t) * MOE_RG + lane];
-      }
-      if (clamp > 1e-6f) {  // deepseek4 order: up symmetric, gate one-sided, before SiLU
-        up = fmaxf(fminf(up, clamp), -clamp);
-        g = fminf(g, clamp);
-      }
-      const float h = u.valid ? __fmul_rn(__fdiv_rn(g, 1.0f + expf(-g)), up) : 0.0f;
-      const int hrow = u.row0 + i0 + t;
-      // Q8_0 over each 32-lane half (two h blocks per row group)
-      float amax = fabsf(h);
-      amax = fmaxf(amax, dpp_f<0xB1>(amax));
-      amax = fmaxf(amax, dpp_f<0x4E>(amax));
-      amax = fmaxf(amax, dpp_f<0x141>(amax));
-      amax = fmaxf(amax, dpp_f<0x140>(amax));
-      const float am_lo = fmaxf(readlane_f(amax, 0), readlane_f(amax, 16));
-      const float am_hi = fmaxf(readlane_f(amax, 32), readlane_f(amax, 48));
-      const float am = lane < 32 ? am_lo : am_hi;
-      const float qv = q8_code(h, am);
-      const float qhi = __shfl_down(qv, 16);
-      const size_t blk = (size_t)hrow * (size_t)(F / MOE_QK) + 2 * blockIdx.x + (lane >> 5);
-      if ((lane & 31) < 16) hq[blk * 16 + (lane & 15)] = pack_f16x2(qv, qhi);
-      if ((lane & 31) == 0) hd[blk] = (float)q8_scale_f16(am);
-      if (htap) htap[(size_t)hrow * F + blockIdx.x * MOE_RG + lane] = h;
+    bsel bs[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+      bs[p] = make_bsel(lane, 4 + 2 * p * NBW * MOE_XSW, 4 + (2 * p + 1) * NBW * MOE_XSW, 2 * p * NBW,
+                        (2 * p + 1) * NBW, 2 * p < nt, 2 * p + 1 < nt, 0);
+    f32x4_t acc[NP][4];
+    kloop<4, NP>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
+    __syncthreads();  // every wave is done with its staged rows before red overwrites them
+    const int gb = lane >> 4, tp = (lane >> 3) & 1;
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float v = col8_sum(acc[p][i][r]);
+          if ((lane & 7) == 0) red[((wave * 4 + i) * NTOK + 2 * p + tp) * MOE_TILE + 4 * gb + r] = v;
+        }
+    __syncthreads();
+    // epilogue: wave w takes token slots 2w, 2w+1 (lane half = token, lane j = row)
+    for (int t = 2 * wave; t < nt; t += 2 * MOE_GRP_WAVES) {
+      const int ts = t + (lane >> 5);
+      const int j = lane & 31, ti = j >> 4, rr = j & 15;
+      const bool live = ts < nt;
+      float gsum = 0.0f, usum = 0.0f;
+      if (live)
+        for (int w = 0; w < MOE_GRP_WAVES; w++) {
+          gsum += red[((w * 4 + ti) * NTOK + ts) * MOE_TILE + rr];
+          usum += red[((w * 4 + 2 + ti) * NTOK + ts) * MOE_TILE + rr];
+        }
+      const float h = live && un.valid ? swiglu(gsum, usum, clamp) : 0.0f;
+      const int hrow = un.row0 + i0 + (live ? ts : 0);
+      h_unit_store(h, live, hs + ((size_t)hrow * U + u) * MOE_XSW, hd + (size_t)hrow * U + u, lane);
+      if (htap && live) htap[(size_t)hrow * F + (size_t)u * MOE_UNIT + j] = h;
     }
     __syncthreads();
   }
 }
 
-// ---------------------------------------------------------------------------
-// down (x router weight).  grid (H/64, ny), MOE_DN_WAVES waves.
-// y[hrow][H] = (down_row . h[hrow]) * w   (w = wts[pair] for routed rows in
-// grouped mode, wts[s] in decode mode, none for the shared expert).
-template <int NT>
-__global__ __launch_bounds__(64 * MOE_DN_WAVES) void k_down(
-    const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hq,
-    const float *__restrict__ hd, int grouped, const int32_t *__restrict__ ids,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm, const int32_t *__restrict__ act,
-    const float *__restrict__ wts, int k, int E, int shared, int T, int F, int H, float *__restrict__ y) {
-  extern __shared__ __align__(16) uint32_t lds[];
-  const int KB = F / MOE_QK, KQ = KB / 4, NBW = max_wave_blocks(KB, MOE_DN_WAVES);
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int P = T * k;
-  const unit_t u = unit_of(blockIdx.y, gridDim.y, grouped, ids, offsets, act, k, E, shared, P, T);
-  if (!u.valid && grouped) return;
-  int q0, q1;
-  wave_groups(KQ, MOE_DN_WAVES, wave, q0, q1);
-  const int nbw = 4 * (q1 - q0);
-  uint32_t *q_s = lds + (size_t)wave * NT * NBW * 16;
-  float *d_s = reinterpret_cast<float *>(lds + (size_t)MOE_DN_WAVES * NT * NBW * 16) + (size_t)wave * NT * NBW;
-  float *red = reinterpret_cast<float *>(lds + (size_t)MOE_DN_WAVES * NT * NBW * 17);  // [waves][NT][64]
-
-  const int G = H / MOE_RG;
-  const size_t grp = (size_t)u.mat * G + blockIdx.x;
-  const uint4 *const nibs[1] = {nib_d + grp * KB * MOE_RG + (size_t)4 * q0 * MOE_RG};
-  const uint32_t *const scs[1] = {sc_d + grp * KQ * MOE_RG + (size_t)q0 * MOE_RG};
-
-  const int nq = q1 - q0;
-  for (int i0 = 0; i0 < u.nrows; i0 += NT) {
-    const int nt = u.nrows - i0 < NT ? u.nrows - i0 : NT;
-    wgroup<1> ring[2];
-    ring_prime<1, 2>(ring, nibs, scs, nq, lane);
-#pragma unroll
-    for (int t = 0; t < NT; t++) {
-      if (t < nt && u.valid) {
-        const size_t hrow = (size_t)(u.row0 + i0 + t);
-        stage_copy(hq + (hrow * KB + 4 * q0) * 16, hd + hrow * KB + 4 * q0, nbw, q_s + (size_t)t * NBW * 16,
-                   d_s + (size_t)t * NBW, lane);
-      } else {
-        stage_zero(nbw, q_s + (size_t)t * NBW * 16, d_s + (size_t)t * NBW, lane);
-      }
-    }
-    float acc[1][NT];
-    rows_dot<1, NT, 2>(ring, nibs, scs, nq, q_s, d_s, NBW, lane, acc);
-#pragma unroll
-    for (int t = 0; t < NT; t++) red[(wave * NT + t) * MOE_RG + lane] = acc[0][t];
-    __syncthreads();
-    if (wave < nt) {
-      const int t = wave;
-      float v = 0.0f;
-      for (int w = 0; w < MOE_DN_WAVES; w++) v += red[(w * NT + t) * MOE_RG + lane];
-      const int hrow = u.row0 + i0 + t;
-      if (!u.shared) {
-        const float wt = grouped ? wts[perm[hrow]] : wts[hrow];
-        v = __fmul_rn(v, wt);
-      }
-      if (!u.valid) v = 0.0f;
-      y[(size_t)hrow * H + (size_t)blockIdx.x * MOE_RG + lane] = v;
-    }
-    __syncthreads();
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Decode gate/up (T == 1) as split-K one-wave workgroups.
-//
-// A decode call is small (the 9 touched experts of a V3 layer) and HBM-bound
-// only if every CU streams the same share: a workgroup per (slot, row group)
-// leaves the chip unevenly loaded (288 units on 256 CUs).  So the reduction
-// K of every (slot, row group) unit is cut into C chunks, one single-wave
-// workgroup each (2304 equal workgroups for V3 gate/up).
-// Each writes its 64 partial sums; the last workgroup of a unit to finish
-// adds the chunks in chunk order and finishes the unit, then resets the
-// ticket for the next call.  No workgroup ever waits on another, and the
-// sums do not depend on arrival order.
-//
-// Visibility without cache write-backs: every access to the shared partials
-// and tickets is an agent-scope atomic (stores and loads carry sc1, so they
-// are coherent across the XCDs' L2s on their own).  A chunk's stores have
-// completed (s_waitcnt vmcnt(0)) before its ticket increment is issued, and
-// the last chunk's loads are issued after its increment has returned, so the
-// last chunk reads every other chunk's partials.  (An acq_rel ticket would
-// also be correct, but its release writes back the whole L2 of the XCD --
-// buffer_wbl2 -- once per workgroup, which measured 4x slower.)
-#define MOE_DEC_DEPTH 3  // groups of 4 blocks in the load ring
-
-__device__ __forceinline__ void store_shared(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// All of this wave's stores complete, then lane 0 takes a ticket; the
-// ticket's previous value is returned wave-uniform (an SGPR via readfirstlane,
-// read while every lane is active), so branches on it are scalar branches.
-__device__ __forceinline__ int ticket_take(int32_t *ctr, int lane) {
-  __builtin_amdgcn_s_waitcnt(0);
-  int t = 0;
-  if (lane == 0) t = __hip_atomic_fetch_add(ctr, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return __builtin_amdgcn_readfirstlane(t);
-}
-
-__device__ __forceinline__ float load_acquired(const float *p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// gate/up -> SwiGLU -> Q8_0(h).  grid S*G*C (G = F/64), 64 threads;
-// block id = (s*G + g)*C + c.  part: [S*G][C][2][64] f32, ctr: [S*G].
-__global__ __launch_bounds__(64) void k_gate_up_dec(
-    const uint4 *__restrict__ nib_g, const uint4 *__restrict__ nib_u, const uint32_t *__restrict__ sc_g,
-    const uint32_t *__restrict__ sc_u, const float *__restrict__ x, const int32_t *__restrict__ ids, int k, int E,
-    int F, int H, int C, float clamp, float *__restrict__ part, int32_t *__restrict__ ctr,
-    uint32_t *__restrict__ hq, float *__restrict__ hd, float *__restrict__ htap) {
-  extern __shared__ __align__(16) uint32_t lds[];
-  const int KB = H / MOE_QK, KQ = KB / 4, G = F / MOE_RG;
-  const int lane = threadIdx.x;
-  const int unit = blockIdx.x / C, c = blockIdx.x - unit * C;
-  const int s = unit / G, g = unit - s * G;
-  int e = s < k ? ids[s] : E;
-  const bool valid = s >= k || (unsigned)e < (unsigned)E;  // an out-of-range id reads nothing, yields 0
-  e = valid ? e : 0;
-  int q0, q1;
-  wave_groups(KQ, C, c, q0, q1);
-  const int nq = q1 - q0;
-  const size_t grp = (size_t)e * G + g;
-  const uint4 *const nibs[2] = {nib_g + (grp * KB + 4 * q0) * MOE_RG, nib_u + (grp * KB + 4 * q0) * MOE_RG};
-  const uint32_t *const scs[2] = {sc_g + (grp * KQ + q0) * MOE_RG, sc_u + (grp * KQ + q0) * MOE_RG};
-  wgroup<2> ring[MOE_DEC_DEPTH];
-  ring_prime<2, MOE_DEC_DEPTH>(ring, nibs, scs, nq, lane);
-  uint32_t *q_s = lds;
-  float *d_s = reinterpret_cast<float *>(lds + (size_t)4 * nq * 16);
-  stage_quantize(x + (size_t)4 * q0 * MOE_QK, 4 * nq, q_s, d_s, lane);
-  __syncthreads();
-  float acc[2][1];
-  rows_dot<2, 1, MOE_DEC_DEPTH>(ring, nibs, scs, nq, q_s, d_s, 0, lane, acc);
-  float *pp = part + ((size_t)unit * C + c) * 2 * MOE_RG;
-  store_shared(pp + lane, valid ? acc[0][0] : 0.0f);
-  store_shared(pp + MOE_RG + lane, valid ? acc[1][0] : 0.0f);
-  if (ticket_take(ctr + unit, lane) != C - 1) return;
-  // last chunk of this unit: sum the chunks in order, clamp, SwiGLU, Q8_0
-  float gs = 0.0f, us = 0.0f;
-  const float *pu = part + (size_t)unit * C * 2 * MOE_RG;
-  for (int cc = 0; cc < C; cc++) {
-    gs += load_acquired(pu + (size_t)cc * 2 * MOE_RG + lane);
-    us += load_acquired(pu + (size_t)cc * 2 * MOE_RG + MOE_RG + lane);
-  }
-  if (lane == 0) __hip_atomic_store(ctr + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  if (clamp > 1e-6f) {  // deepseek4 order: up symmetric, gate one-sided, before SiLU
-    us = fmaxf(fminf(us, clamp), -clamp);
-    gs = fminf(gs, clamp);
-  }
-  const float h = valid ? __fmul_rn(__fdiv_rn(gs, 1.0f + expf(-gs)), us) : 0.0f;
-  float amax = fabsf(h);
-  amax = fmaxf(amax, dpp_f<0xB1>(amax));
-  amax = fmaxf(amax, dpp_f<0x4E>(amax));
-  amax = fmaxf(amax, dpp_f<0x141>(amax));
-  amax = fmaxf(amax, dpp_f<0x140>(amax));
-  const float am = lane < 32 ? fmaxf(readlane_f(amax, 0), readlane_f(amax, 16))
-                             : fmaxf(readlane_f(amax, 32), readlane_f(amax, 48));
-  const float qv = q8_code(h, am);
-  const float qhi = __shfl_down(qv, 16);
-  const size_t blk = (size_t)s * (size_t)(F / MOE_QK) + 2 * g + (lane >> 5);
-  if ((lane & 31) < 16) hq[blk * 16 + (lane & 15)] = pack_f16x2(qv, qhi);
-  if ((lane & 31) == 0) hd[blk] = (float)q8_scale_f16(am);
-  if (htap) htap[(size_t)s * F + (size_t)g * MOE_RG + lane] = h;
-}
-
-// Decode down with the top-k combine fused (T == 1).  grid H/16, 64*S
-// threads: wave s computes slot s (s == k: the shared expert) for 16 output
-// rows; lane = (row r16 = lane & 15, K-quarter kq = lane >> 4), quarter kq
-// takes the 4-block groups g = 4j + kq.  The quarters are summed with two
-// lane swaps, each slot's rows are scaled by its router weight, and the
-// slots are added in slot order, ((y0 + y1) + ...) + shared (the
-// reference's trunk ADD chain, nano-glm/lib/models/glm_dsa/moe_block.h:120-131).
-// per_slot: out[s][H] = y_s (the MUL node of the reference's split) instead.
-// A 16-row workgroup reads 256 B runs of every 1 KiB block row (the layout's
-// 64-row groups); all slots of a row live in one workgroup, so nothing
-// crosses workgroups.  LDS: per slot KQ groups of 272 B (4 h blocks + 16 B so
-// the four quarters' reads fall in different banks) + KB scales, then the
-// [S][16] slot rows.
-#define MOE_DN_GROUP_BYTES 272
-
-__device__ __forceinline__ void dq_load(wgroup<1> &g, const uint4 *__restrict__ nib, const uint32_t *__restrict__ sc,
-                                        int grp, int lane64) {
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-    g.w[0][i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4_t *>(nib + (size_t)(4 * grp + i) * MOE_RG + lane64));
-  g.e[0] = __builtin_nontemporal_load(sc + (size_t)grp * MOE_RG + lane64);
-}
-
-__global__ __launch_bounds__(1024) void k_down_decode(
-    const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hq,
+// Decode down with the top-k combine (T == 1).  One workgroup per 16-row tile
+// of H with one wave per slot (S <= 16): wave s streams the tile of its
+// expert's down matrix over all of F against its slot's staged h and scales
+// the rows by the router weight; the slot rows meet in LDS and are added in
+// slot order, ((y0 + y1) + ...) + shared (the reference's trunk ADD chain,
+// nano-glm/lib/models/glm_dsa/moe_block.h:120-131).  per_slot: out[s][H] =
+// y_s (the MUL node of the reference's split) instead.
+// grid H/16, 64*S threads.  LDS: per wave [zero 4][xs F/32*16][dy F/32]
+// dwords, then ys[S][16].
+__global__ __launch_bounds__(1024) void k_down_dec(
+    const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hs,
     const float *__restrict__ hd, const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int E,
     int S, int F, int H, int per_slot, float *__restrict__ out) {
   extern __shared__ __align__(16) uint32_t lds[];
-  const int KB = F / MOE_QK, KQ = KB / 4;
+  const int NQ = F / 128, NQ4 = moe_nq4(NQ), tiles = H / MOE_TILE, U = F / MOE_UNIT;
+  const int nb = F / MOE_QK, wave_words = 4 + nb * (MOE_XSW + 1);
   const int lane = threadIdx.x & 63, s = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int r16 = lane & 15, kq = lane >> 4;
-  const size_t slot_bytes = (size_t)KQ * MOE_DN_GROUP_BYTES + (size_t)KB * 4;
-  uint8_t *base = reinterpret_cast<uint8_t *>(lds) + (size_t)s * slot_bytes;
-  float *d_s = reinterpret_cast<float *>(base + (size_t)KQ * MOE_DN_GROUP_BYTES);
-  float *ys = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(lds) + (size_t)S * slot_bytes);  // [S][16]
-
+  const int tile = blockIdx.x;
   int e = s < k ? ids[s] : E;
   const bool valid = s >= k || (unsigned)e < (unsigned)E;  // an out-of-range id reads nothing, yields 0
   e = valid ? e : 0;
-  const int G = H / MOE_RG;
-  const int grp64 = blockIdx.x >> 2, lane64 = (blockIdx.x & 3) * 16 + r16;
-  const size_t mg = (size_t)e * G + grp64;
-  const uint4 *nib = nib_d + mg * KB * MOE_RG;
-  const uint32_t *sc = sc_d + mg * KQ * MOE_RG;
-  const int nj = (KQ + 3) / 4;
-
-  // first weight group in flight before the h staging
-  wgroup<1> ga, gb;
-  dq_load(ga, nib, sc, kq < KQ ? kq : KQ - 1, lane64);
-  // stage h of this slot: block b -> group b/4 at 272 B, offset (b%4)*64
-  const uint4 *hsrc = reinterpret_cast<const uint4 *>(hq + (size_t)s * KB * 16);
-  const int n16 = KB * 4;  // 16-byte pieces of this slot's h
-  for (int i0 = 0; i0 < n16; i0 += 256) {
-    uint32_t off[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {  // a piece past the end lands in group 0's (unread) pad
-      const int i = i0 + 64 * r + lane;
-      const int b = i >> 2, part = i & 3;
-      off[r] = i < n16 ? (uint32_t)((b >> 2) * MOE_DN_GROUP_BYTES + (b & 3) * 64 + part * 16) : 256u;
-    }
-    uint4 v[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {  // all four loads in flight, clamped in range
-      const int i = i0 + 64 * r + lane;
-      v[r] = hsrc[i < n16 ? i : n16 - 1];
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int r = 0; r < 4; r++) *reinterpret_cast<uint4 *>(base + off[r]) = v[r];
-  }
-  for (int b = lane; b < KB; b += 64) d_s[b] = hd[(size_t)s * KB + b];
+  const wstream ws[1] = {make_wstream(nib_d, sc_d, (size_t)e * tiles + tile, NQ, NQ4)};
+  kring<1> ring;
+  kloop_prime<1>(ring, ws, 0, NQ, lane);
+  uint32_t *xs = lds + (size_t)s * wave_words;
+  float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)nb * MOE_XSW);
+  float *ys = reinterpret_cast<float *>(lds + (size_t)S * wave_words);  // [S][16]
+  if (lane < 4) xs[lane] = 0u;
+  stage_copy<false>(hs + (size_t)s * U * MOE_XSW, hd + (size_t)s * U, nb, xs + 4, dy, lane);
   __syncthreads();
-
-  float acc = 0.0f;
-  for (int j = 0;; j += 2) {
-    const int g0 = 4 * j + kq, g1 = 4 * j + 4 + kq, g2 = 4 * j + 8 + kq;
-    dq_load(gb, nib, sc, g1 < KQ ? g1 : KQ - 1, lane64);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-      float a[1][1];
-      a[0][0] = 0.0f;
-      dot_group<1, 1>(ga, 0, reinterpret_cast<const uint32_t *>(base + (size_t)(g0 < KQ ? g0 : 0) * MOE_DN_GROUP_BYTES),
-                      d_s + 4 * (g0 < KQ ? g0 : 0), 0, a);
-      acc += g0 < KQ ? a[0][0] : 0.0f;
-    }
-    if (j + 1 >= nj) break;
-    dq_load(ga, nib, sc, g2 < KQ ? g2 : KQ - 1, lane64);
-    __builtin_amdgcn_sched_barrier(0);
-    {
-      float a[1][1];
-      a[0][0] = 0.0f;
-      dot_group<1, 1>(gb, 0, reinterpret_cast<const uint32_t *>(base + (size_t)(g1 < KQ ? g1 : 0) * MOE_DN_GROUP_BYTES),
-                      d_s + 4 * (g1 < KQ ? g1 : 0), 0, a);
-      acc += g1 < KQ ? a[0][0] : 0.0f;
-    }
-    if (j + 2 >= nj) break;
+  const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
+  f32x4_t acc[1][1];
+  kloop<1, 1>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
+  const int gb = lane >> 4;
+  const float wt = s < k ? wts[s] : 1.0f;
+  float v[4];
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    v[r] = col8_sum(acc[0][0][r]);
+    if (s < k) v[r] = __fmul_rn(v[r], wt);
+    if (!valid) v[r] = 0.0f;
   }
-  // sum the four K-quarters: (q0 + q1) + (q2 + q3) in every quarter's lanes
-  acc += __shfl_xor(acc, 16);
-  acc += __shfl_xor(acc, 32);
-  float v = valid ? acc : 0.0f;
-  if (s < k) v = __fmul_rn(v, wts[s]);
-  const int row = blockIdx.x * 16 + r16;
+  const int row0 = tile * MOE_TILE + 4 * gb;
   if (per_slot) {
-    if (lane < 16) out[(size_t)s * H + row] = v;
+    if ((lane & 15) == 0)
+#pragma unroll
+      for (int r = 0; r < 4; r++) out[(size_t)s * H + row0 + r] = v[r];
     return;
   }
-  if (lane < 16) ys[s * 16 + lane] = v;
+  if ((lane & 15) == 0)
+#pragma unroll
+    for (int r = 0; r < 4; r++) ys[s * MOE_TILE + 4 * gb + r] = v[r];
   __syncthreads();
-  if (threadIdx.x < 16) {
+  if (threadIdx.x < MOE_TILE) {
     float o = ys[threadIdx.x];
-    for (int q = 1; q < S; q++) o = __fadd_rn(o, ys[q * 16 + threadIdx.x]);
-    out[blockIdx.x * 16 + threadIdx.x] = o;
+    for (int q = 1; q < S; q++) o = __fadd_rn(o, ys[q * MOE_TILE + threadIdx.x]);
+    out[(size_t)tile * MOE_TILE + threadIdx.x] = o;
   }
 }
 
-static inline size_t down_decode_lds_bytes(int F, int S) {
-  const int KB = F / MOE_QK, KQ = KB / 4;
-  return (size_t)S * ((size_t)KQ * MOE_DN_GROUP_BYTES + (size_t)KB * 4) + (size_t)S * 16 * 4;
+// Grouped down (T > 1, x router weight): one workgroup of 4 waves per
+// (32-row unit of H, expert), the waves splitting F; partials meet in LDS.
+// y[hrow][H] = (down_row . h[hrow]) * w   (w = wts[pair] for routed rows).
+// grid (H/32, ny), 256 threads.
+template <int NP>
+__global__ __launch_bounds__(64 * MOE_GRP_WAVES) void k_down_grp(
+    const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hs,
+    const float *__restrict__ hd, const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm,
+    const int32_t *__restrict__ act, const float *__restrict__ wts, int k, int E, int shared, int T, int F, int H,
+    float *__restrict__ y) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  constexpr int NTOK = 2 * NP;
+  const int NQ = F / 128, NQ4 = moe_nq4(NQ), U = F / MOE_UNIT, tiles = H / MOE_TILE;
+  const int NBW = wave_blocks(NQ, MOE_GRP_WAVES);
+  const int wave_words = 4 + NTOK * NBW * (MOE_XSW + 1);
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int P = T * k;
+  const unit_t un = unit_of(blockIdx.y, gridDim.y, true, nullptr, offsets, act, k, E, shared, P, T);
+  if (!un.valid) return;
+  const int u = blockIdx.x;
+  int q0, q1;
+  wave_quads(NQ, MOE_GRP_WAVES, wave, q0, q1);
+  const int nb = 4 * (q1 - q0);
+  uint32_t *xs = lds + (size_t)wave * wave_words;
+  float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)NTOK * NBW * MOE_XSW);
+  float *red = reinterpret_cast<float *>(lds);  // [wave][2 tiles][NTOK][16]
+  const size_t t0 = (size_t)un.mat * tiles + 2 * u;
+  const wstream ws[2] = {make_wstream(nib_d, sc_d, t0, NQ, NQ4), make_wstream(nib_d, sc_d, t0 + 1, NQ, NQ4)};
+  for (int i0 = 0; i0 < un.nrows; i0 += NTOK) {
+    const int nt = un.nrows - i0 < NTOK ? un.nrows - i0 : NTOK;
+    kring<2> ring;
+    kloop_prime<2>(ring, ws, q0, q1, lane);
+    if (lane < 4) xs[lane] = 0u;
+    for (int t = 0; t < nt; t++) {
+      const size_t hrow = (size_t)(un.row0 + i0 + t);
+      stage_copy<false>(hs + (hrow * U + (size_t)4 * q0) * MOE_XSW, hd + hrow * U + (size_t)4 * q0, nb,
+                        xs + 4 + (size_t)t * NBW * MOE_XSW, dy + (size_t)t * NBW, lane);
+    }
+    __syncthreads();
+    bsel bs[NP];
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+      bs[p] = make_bsel(lane, 4 + 2 * p * NBW * MOE_XSW, 4 + (2 * p + 1) * NBW * MOE_XSW, 2 * p * NBW,
+                        (2 * p + 1) * NBW, 2 * p < nt, 2 * p + 1 < nt, 0);
+    f32x4_t acc[NP][2];
+    kloop<2, NP>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
+    __syncthreads();
+    const int gb = lane >> 4, tp = (lane >> 3) & 1;
+#pragma unroll
+    for (int p = 0; p < NP; p++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const float v = col8_sum(acc[p][i][r]);
+          if ((lane & 7) == 0) red[((wave * 2 + i) * NTOK + 2 * p + tp) * MOE_TILE + 4 * gb + r] = v;
+        }
+    __syncthreads();
+    // thread (token slot t = idx / 32, row j = idx % 32)
+    for (int idx = threadIdx.x; idx < nt * MOE_UNIT; idx += 64 * MOE_GRP_WAVES) {
+      const int t = idx >> 5, j = idx & 31, ti = j >> 4, rr = j & 15;
+      float v = 0.0f;
+      for (int w = 0; w < MOE_GRP_WAVES; w++) v += red[((w * 2 + ti) * NTOK + t) * MOE_TILE + rr];
+      const int hrow = un.row0 + i0 + t;
+      if (!un.shared) v = __fmul_rn(v, wts[perm[hrow]]);
+      y[(size_t)hrow * H + (size_t)u * MOE_UNIT + j] = v;
+    }
+    __syncthreads();
+  }
 }
 
-// Chunks per unit for the split-K decode kernels: about 9 single-wave
-// workgroups per CU in all, each chunk at least one group of 4 blocks.
-static inline int decode_chunks(int units, int KQ, int n_cu) {
-  int c = (9 * n_cu + units / 2) / units;
-  c = c < 1 ? 1 : c;
-  return c > KQ ? KQ : c;
+// LDS bytes of the kernels.
+static inline size_t grp_lds_bytes(int K, int NP, int streams) {
+  const int NBW = wave_blocks(K / 128, MOE_GRP_WAVES);
+  const size_t stage = ((size_t)4 + (size_t)2 * NP * NBW * (MOE_XSW + 1)) * 4 * MOE_GRP_WAVES;
+  const size_t red = (size_t)MOE_GRP_WAVES * streams * 2 * NP * MOE_TILE * 4;
+  return stage > red ? stage : red;
 }
-
-// LDS bytes of the two kernels (activations + partials).
-static inline size_t gate_up_lds_bytes(int H, int NT) {
-  const int NBW = max_wave_blocks(H / MOE_QK, MOE_GU_WAVES);
-  return (size_t)MOE_GU_WAVES * NT * NBW * 68 + (size_t)MOE_GU_WAVES * 2 * NT * MOE_RG * 4;
-}
-static inline size_t down_lds_bytes(int F, int NT) {
-  const int NBW = max_wave_blocks(F / MOE_QK, MOE_DN_WAVES);
-  return (size_t)MOE_DN_WAVES * NT * NBW * 68 + (size_t)MOE_DN_WAVES * NT * MOE_RG * 4;
+static inline size_t down_dec_lds_bytes(int F, int S) {
+  const int nb = F / MOE_QK;
+  return ((size_t)S * (4 + (size_t)nb * (MOE_XSW + 1)) + (size_t)S * MOE_TILE) * 4;
 }
 
 // ---------------------------------------------------------------------------
-// test hook: the product quantizer (stage_quantize) over n_blocks blocks of
-// a flat f32 array, 64 blocks per workgroup of one wave; ggml's byte layout.
+// test hook: the product quantizer (stage_quant) over n_blocks blocks of a
+// flat f32 array, 32 blocks per single-wave workgroup, decoded back to
+// ggml's block_q8_0 bytes (q = 16*hi + lo).
 __global__ __launch_bounds__(64) void k_debug_quantize(const float *__restrict__ x, int n_blocks,
                                                        int8_t *__restrict__ qs, uint16_t *__restrict__ d) {
-  __shared__ __align__(16) uint32_t q_s[64 * 16];
-  __shared__ float d_s[64];
+  __shared__ __align__(16) uint32_t xs[32 * MOE_XSW];
+  __shared__ float dy[32];
   const int lane = threadIdx.x;
-  const int b0 = blockIdx.x * 64;
-  const int nb = n_blocks - b0 < 64 ? n_blocks - b0 : 64;
-  stage_quantize(x + (size_t)b0 * MOE_QK, nb, q_s, d_s, lane);
+  const int b0 = blockIdx.x * 32;
+  const int nb = n_blocks - b0 < 32 ? n_blocks - b0 : 32;
+  stage_quant(x + (size_t)b0 * MOE_QK, nb, xs, dy, lane);
   __syncthreads();
-  for (int i = lane; i < nb * 16; i += 64) {
-    const f16x2_t p = __builtin_bit_cast(f16x2_t, q_s[i]);
-    const size_t b = (size_t)b0 + (i >> 4);
-    const int j = i & 15;
-    qs[b * MOE_QK + j] = (int8_t)(int)(float)p.x;
-    qs[b * MOE_QK + j + 16] = (int8_t)(int)(float)p.y;
+  for (int i = lane; i < nb * 32; i += 64) {
+    const int b = i >> 5, e = i & 31;  // MFMA K offset e of block b
+    const uint32_t wh = xs[b * MOE_XSW + (e >> 2)], wl = xs[b * MOE_XSW + 8 + (e >> 2)];
+    const int sel = e & 3;
+    const float hv = __builtin_amdgcn_cvt_f32_fp8((int)(wh >> (8 * sel)), 0);
+    const float lv = __builtin_amdgcn_cvt_f32_fp8((int)(wl >> (8 * sel)), 0);
+    const int elem = (e >> 1) + 16 * (e & 1);
+    qs[(size_t)(b0 + b) * MOE_QK + elem] = (int8_t)(int)(16.0f * hv + lv);
   }
-  if (lane < nb) d[(size_t)b0 + lane] = __builtin_bit_cast(uint16_t, (_Float16)d_s[lane]);
+  if (lane < nb) d[(size_t)b0 + lane] = __builtin_bit_cast(uint16_t, (_Float16)dy[lane]);
 }

@@ -2,15 +2,17 @@
 //
 // ggml stores an expert matrix of R rows x K reduction as R*KB 17-byte
 // blocks {uint8 e; uint8 qs[16]} (KB = K/32), row-major.  On the device the
-// two parts are split into the row-interleaved layout the vecmat kernels
-// stream (kernels_rows.h):
-//   nib[grp][b][l]        uint4  qs of block b of row 64*grp + l (bytes unchanged)
-//   sc [grp][b/4][l][b%4] uint8  e  of the same block
-// for every row group grp = r/64 of every expert, experts back to back.
-// The reference splits the same two planes for the same reason
-// (moe-serv/src/moe_tp.h:235-278: nibble plane + scale plane, columns
-// interleaved for its column-per-thread kernel); here a lane owns a row and
-// a wave reads 64 rows' block b as one 1 KiB run.
+// two parts are split into the tiled layout the MFMA kernels stream
+// (kernels_rows.h), with NQ = KB/4 quads of 4 blocks and NQ4 = ceil(NQ/4):
+//   nib[tile][q][l]        uint4  qs of block 4q + l/16 of row 16*tile + l%16
+//   sc [tile][q/4][l][q%4] uint8  e  of the same block
+// for every 16-row tile of every expert, experts back to back (an expert's
+// exponent plane is R/16 * NQ4 * 256 bytes; the bytes of quads past NQ in
+// the last dword group are padding).  The reference splits the same two
+// planes for the same reason (moe-serv/src/moe_tp.h:235-278: nibble plane +
+// scale plane, interleaved for its kernel's access pattern); here one wave
+// reads a (tile, quad) as one contiguous KiB, which is the A-operand lane
+// layout of the 16x16x128 scaled MFMA.
 //
 // Every kernel below runs one thread per block of one expert matrix, indexed
 // by its position o in the device layout (so the device-side accesses are
@@ -19,28 +21,37 @@
 
 #include "device_common.h"
 
+// Exponent-plane bytes of one expert matrix of R rows and KB blocks per row.
+__host__ __device__ __forceinline__ uint64_t sc_plane_bytes(int R, int KB) {
+  const int NQ = KB / 4;
+  return (uint64_t)(R / 16) * (uint64_t)((NQ + 3) / 4) * 256u;
+}
+
 __device__ __forceinline__ void layout_of(uint64_t o, int KB, uint64_t &i, uint64_t &sc_byte) {
+  const int NQ = KB >> 2, NQ4 = (NQ + 3) >> 2;
   const uint32_t l = (uint32_t)(o & 63u);
-  const uint64_t gb = o >> 6;  // grp*KB + b
-  const uint64_t g = gb / (uint64_t)KB;
-  const uint32_t b = (uint32_t)(gb - g * (uint64_t)KB);
-  const uint64_t r = g * 64u + l;
+  const uint64_t tq = o >> 6;  // tile*NQ + q
+  const uint64_t tile = tq / (uint64_t)NQ;
+  const uint32_t q = (uint32_t)(tq - tile * (uint64_t)NQ);
+  const uint64_t r = tile * 16u + (l & 15u);
+  const uint32_t b = 4u * q + (l >> 4);
   i = r * (uint64_t)KB + b;
-  sc_byte = ((g * (uint64_t)(KB / 4) + (b >> 2)) * 64u + l) * 4u + (b & 3u);
+  sc_byte = ((tile * (uint64_t)NQ4 + (q >> 2)) * 64u + l) * 4u + (q & 3u);
 }
 
 // ggml 17-byte blocks of consecutive expert matrices (per_exp = R*KB blocks
 // each, n_blocks in all) -> (nib, sc) of the same experts.
+// sc points at the first expert's exponent plane (sc_per_exp bytes each).
 __global__ __launch_bounds__(256) void k_repack_blocks(const uint8_t *__restrict__ src, uint64_t n_blocks,
-                                                       uint64_t per_exp, int KB, uint4 *__restrict__ nib,
-                                                       uint8_t *__restrict__ sc) {
+                                                       uint64_t per_exp, uint64_t sc_per_exp, int KB,
+                                                       uint4 *__restrict__ nib, uint8_t *__restrict__ sc) {
   const uint64_t o = (uint64_t)blockIdx.x * 256u + threadIdx.x;
   if (o >= n_blocks) return;
   const uint64_t e = o / per_exp, base = e * per_exp;
   uint64_t i, sb;
   layout_of(o - base, KB, i, sb);
   i += base;
-  sb += base;
+  sb += e * sc_per_exp;
   const uint8_t *b = src + i * 17u;
   uint32_t w[4];
 #pragma unroll

@@ -31,8 +31,9 @@ enum { T_GATE = 0, T_UP = 1, T_DOWN = 2 };
 // experts, in the row-interleaved layout of kernels_weights.h.
 struct dev_mat {
   uint4 *nib = nullptr;   // E'*R*KB 16-byte nibble payloads
-  uint8_t *sc = nullptr;  // E'*R*KB E8M0 exponents
+  uint8_t *sc = nullptr;  // E' exponent planes of sc_per_exp bytes
   int rows = 0, kb = 0;
+  uint64_t sc_per_exp = 0;
 };
 
 struct dev_layer {
@@ -45,17 +46,13 @@ struct dev_layer {
 struct scratch {
   // sized for (T, H, F, E, k)
   int T = 0, H = 0, F = 0, E = 0, k = 0;
-  uint32_t *hq = nullptr; float *hd = nullptr;     // [P+T][F/32][16], [P+T][F/32]
+  uint32_t *hq = nullptr; float *hd = nullptr;     // staged h: [P+T][F/32][16] dwords, [P+T][F/32]
   float *htap = nullptr;                           // [P+T][F]
   float *y = nullptr;                              // [P+T][H]
   int32_t *grp = nullptr;                          // grouping workspace
   size_t grp_words = 0;
   // split-K decode: chunk partial sums and per-unit tickets (the tickets are
   // zeroed once here and left at zero by every launch)
-  float *part = nullptr;   // split-K gate/up partials
-  size_t part_floats = 0;
-  int32_t *ctr = nullptr;
-  size_t ctr_words = 0;
   // host-boundary staging
   float *x_in = nullptr; int32_t *ids_in = nullptr; float *wts_in = nullptr; float *out_buf = nullptr;
   size_t out_cap = 0;
@@ -193,7 +190,7 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 // scratch
 
 static void scratch_free(scratch &s) {
-  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf, s.part, s.ctr};
+  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   s = scratch();
@@ -222,14 +219,6 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipMalloc(&s.wts_in, P * 4));
   s.out_cap = P * H;
   HIPC(c, hipMalloc(&s.out_buf, s.out_cap * 4));
-  // decode gate/up partials: [S*G_F][C<=H/128][2][64]
-  const size_t S1 = (size_t)k + 1;
-  s.part_floats = S1 * (F / 64) * (H / 128) * 128;
-  HIPC(c, hipMalloc(&s.part, s.part_floats * 4));
-  // tickets: one per (slot, 64-row group of F)
-  s.ctr_words = S1 * (F / 64);
-  HIPC(c, hipMalloc(&s.ctr, s.ctr_words * 4));
-  HIPC(c, hipMemset(s.ctr, 0, s.ctr_words * 4));
   HIPC(c, hipDeviceSynchronize());
   s.T = T; s.H = H; s.F = F; s.E = E; s.k = k;
   return MOE_OK;
@@ -329,8 +318,9 @@ static moe_status layer_alloc(moe_ctx *c, int layer, const moe_layer_desc *d, de
     const size_t nb = (size_t)L.n_mats * rows[t] * kbs[t];
     L.m[t].rows = rows[t];
     L.m[t].kb = kbs[t];
+    L.m[t].sc_per_exp = sc_plane_bytes(rows[t], kbs[t]);
     hipError_t e1 = hipMalloc(&L.m[t].nib, nb * 16);
-    hipError_t e2 = e1 == hipSuccess ? hipMalloc(&L.m[t].sc, nb) : e1;
+    hipError_t e2 = e1 == hipSuccess ? hipMalloc(&L.m[t].sc, (size_t)L.n_mats * L.m[t].sc_per_exp) : e1;
     if (e1 != hipSuccess || e2 != hipSuccess) {
       for (dev_mat &m : L.m) {
         if (m.nib) (void)hipFree(m.nib);
@@ -396,8 +386,9 @@ extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_de
           st = fail(c, MOE_ERR_HIP, "moe_layer_upload: host->device copy failed");
           break;
         }
+        const size_t first = (part == 0 ? e0 : (size_t)d->n_expert);  // expert index of the batch's first matrix
         hipLaunchKernelGGL(k_repack_blocks, dim3(ceil_div((long)n, 256)), dim3(256), 0, 0, stage, (uint64_t)n,
-                           (uint64_t)per_exp, m.kb, m.nib + base + off, m.sc + base + off);
+                           (uint64_t)per_exp, m.sc_per_exp, m.kb, m.nib + base + off, m.sc + first * m.sc_per_exp);
       }
     }
   }
@@ -427,7 +418,7 @@ extern "C" moe_status moe_layer_generate(moe_ctx *c, int layer, const moe_layer_
       const uint64_t key = host_mix64(seed ^ host_mix64(id));
       hipLaunchKernelGGL(k_generate_blocks, dim3(ceil_div((long)per_exp, 256)), dim3(256), 0, 0, key,
                          (uint64_t)per_exp, m.kb, (uint32_t)e_lo, (uint32_t)e_span, m.nib + per_exp * e,
-                         m.sc + per_exp * e);
+                         m.sc + m.sc_per_exp * e);
     }
   }
   if (hipDeviceSynchronize() != hipSuccess) {
@@ -450,7 +441,7 @@ extern "C" moe_status moe_layer_read_blocks(moe_ctx *c, int layer, int tensor, i
   uint8_t *tmp = nullptr;
   HIPC(c, hipMalloc(&tmp, nb * 17));
   hipLaunchKernelGGL(k_unpack_blocks, dim3(ceil_div((long)nb, 256)), dim3(256), 0, 0, m.nib + nb * expert,
-                     m.sc + nb * expert, (uint64_t)nb, m.kb, tmp);
+                     m.sc + m.sc_per_exp * expert, (uint64_t)nb, m.kb, tmp);
   hipError_t e = hipMemcpy(out, tmp, nb * 17, hipMemcpyDeviceToHost);
   (void)hipFree(tmp);
   if (e != hipSuccess) return fail(c, MOE_ERR_HIP, "moe_layer_read_blocks: copy failed");
@@ -509,53 +500,49 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
   return MOE_OK;
 }
 
-// Tokens per workgroup pass of the grouped kernels: as many as fit the
-// 64 KiB of LDS a workgroup can address without an attribute.
-static int pick_nt_gate_up(int H) {
-  if (gate_up_lds_bytes(H, 4) <= 65536) return 4;
-  if (gate_up_lds_bytes(H, 2) <= 65536) return 2;
-  return gate_up_lds_bytes(H, 1) <= 65536 ? 1 : 0;
-}
-static int pick_nt_down(int F) {
-  if (down_lds_bytes(F, 4) <= 65536) return 4;
-  if (down_lds_bytes(F, 2) <= 65536) return 2;
-  return down_lds_bytes(F, 1) <= 65536 ? 1 : 0;
+// Token pairs per pass of the workgroup kernels: as many as fit the 64 KiB of
+// LDS a workgroup can address without an attribute.
+static int pick_np(int K, int streams) {
+  if (grp_lds_bytes(K, 4, streams) <= 65536) return 4;
+  if (grp_lds_bytes(K, 2, streams) <= 65536) return 2;
+  return grp_lds_bytes(K, 1, streams) <= 65536 ? 1 : 0;
 }
 
-// gate/up launch; grouped == 0: decode columns are slots (ids), one token.
-static void launch_gate_up(int NT, dim3 g, hipStream_t st, const dev_layer &L, const float *x, int grouped,
+// gate/up launch; grouped == 0: decode, columns are slots (ids), one token.
+static void launch_gate_up(int NP, dim3 g, hipStream_t st, const dev_layer &L, const float *x, int grouped,
                            const int32_t *ids, const int32_t *offsets, const int32_t *perm, const int32_t *act,
                            int shared, int T, uint32_t *hq, float *hd, float *htap) {
   const moe_layer_desc &d = L.d;
-  const size_t lds = gate_up_lds_bytes(d.hidden, NT);
+  const size_t lds = grp_lds_bytes(d.hidden, NP, 4);
   const uint32_t *scg = reinterpret_cast<const uint32_t *>(L.m[T_GATE].sc);
   const uint32_t *scu = reinterpret_cast<const uint32_t *>(L.m[T_UP].sc);
 #define MOE_GU_ARGS L.m[T_GATE].nib, L.m[T_UP].nib, scg, scu, x, grouped, ids, offsets, perm, act, d.n_used, \
                     d.n_expert, shared, T, d.ffn, d.hidden, d.clamp, hq, hd, htap
-  if (NT == 4) hipLaunchKernelGGL(k_gate_up<4>, g, dim3(64 * MOE_GU_WAVES), lds, st, MOE_GU_ARGS);
-  else if (NT == 2) hipLaunchKernelGGL(k_gate_up<2>, g, dim3(64 * MOE_GU_WAVES), lds, st, MOE_GU_ARGS);
-  else hipLaunchKernelGGL(k_gate_up<1>, g, dim3(64 * MOE_GU_WAVES), lds, st, MOE_GU_ARGS);
+  const dim3 blk(64 * MOE_GRP_WAVES);
+  if (NP == 4) hipLaunchKernelGGL(k_gate_up<4>, g, blk, lds, st, MOE_GU_ARGS);
+  else if (NP == 2) hipLaunchKernelGGL(k_gate_up<2>, g, blk, lds, st, MOE_GU_ARGS);
+  else hipLaunchKernelGGL(k_gate_up<1>, g, blk, lds, st, MOE_GU_ARGS);
 #undef MOE_GU_ARGS
 }
 
-static void launch_down(int NT, dim3 g, hipStream_t st, const dev_layer &L, const uint32_t *hq, const float *hd,
-                        int grouped, const int32_t *ids, const int32_t *offsets, const int32_t *perm,
-                        const int32_t *act, const float *wts, int shared, int T, float *y) {
+static void launch_down_grp(int NP, dim3 g, hipStream_t st, const dev_layer &L, const uint32_t *hq, const float *hd,
+                            const int32_t *offsets, const int32_t *perm, const int32_t *act, const float *wts,
+                            int shared, int T, float *y) {
   const moe_layer_desc &d = L.d;
-  const size_t lds = down_lds_bytes(d.ffn, NT);
+  const size_t lds = grp_lds_bytes(d.ffn, NP, 2);
   const uint32_t *scd = reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc);
-#define MOE_DN_ARGS L.m[T_DOWN].nib, scd, hq, hd, grouped, ids, offsets, perm, act, wts, d.n_used, d.n_expert, \
-                    shared, T, d.ffn, d.hidden, y
-  if (NT == 4) hipLaunchKernelGGL(k_down<4>, g, dim3(64 * MOE_DN_WAVES), lds, st, MOE_DN_ARGS);
-  else if (NT == 2) hipLaunchKernelGGL(k_down<2>, g, dim3(64 * MOE_DN_WAVES), lds, st, MOE_DN_ARGS);
-  else hipLaunchKernelGGL(k_down<1>, g, dim3(64 * MOE_DN_WAVES), lds, st, MOE_DN_ARGS);
+#define MOE_DN_ARGS L.m[T_DOWN].nib, scd, hq, hd, offsets, perm, act, wts, d.n_used, d.n_expert, shared, T, d.ffn, \
+                    d.hidden, y
+  const dim3 blk(64 * MOE_GRP_WAVES);
+  if (NP == 4) hipLaunchKernelGGL(k_down_grp<4>, g, blk, lds, st, MOE_DN_ARGS);
+  else if (NP == 2) hipLaunchKernelGGL(k_down_grp<2>, g, blk, lds, st, MOE_DN_ARGS);
+  else hipLaunchKernelGGL(k_down_grp<1>, g, blk, lds, st, MOE_DN_ARGS);
 #undef MOE_DN_ARGS
 }
 
-// The decode chain for T == 1, two launches: split-K gate/up (+ SwiGLU and
-// Q8_0 of h by the last chunk of each row group), then down with the router
-// weights and the slot-order combine fused (all slots of 16 output rows per
-// workgroup).
+// The decode chain for T == 1, two launches: gate/up per (32-row unit, slot)
+// with SwiGLU and Q8_0 of h, then down per 16-row tile of H with one wave per
+// slot, the router weights and the slot-order combine.
 static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
                                  float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
@@ -565,24 +552,18 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   const int S = k + shared;
   scratch &s = c->sc;
   float *htap = c->taps ? s.htap : nullptr;
-  const int KQh = H / 128, Gf = F / MOE_RG;
-  const int c1 = decode_chunks(S * Gf, KQh, c->n_cu);
-  if ((size_t)S * Gf * c1 * 128 > s.part_floats || (size_t)S * Gf > s.ctr_words)
-    return fail(c, MOE_ERR_INVALID_ARG, "decode: scratch not sized for this shape");
-  const size_t lds1 = (size_t)4 * ((KQh + c1 - 1) / c1) * 68, lds2 = down_decode_lds_bytes(F, S);
-  if (S > 16 || lds2 > 65536) return fail(c, MOE_ERR_UNSUPPORTED, "decode: more than 16 slots or ffn too large");
+  const size_t lds1 = grp_lds_bytes(H, 1, 4), lds2 = down_dec_lds_bytes(F, S);
+  if (S > 16 || lds1 > 65536 || lds2 > 65536)
+    return fail(c, MOE_ERR_UNSUPPORTED, "decode: more than 16 slots, or hidden/ffn too large");
   {
     prof_scope pg(c, K_GU_DECODE, st);
-    hipLaunchKernelGGL(k_gate_up_dec, dim3(S * Gf * c1), dim3(64), lds1, st, L.m[T_GATE].nib, L.m[T_UP].nib,
-                       reinterpret_cast<const uint32_t *>(L.m[T_GATE].sc),
-                       reinterpret_cast<const uint32_t *>(L.m[T_UP].sc), x, ids, k, E, F, H, c1, d.clamp, s.part,
-                       s.ctr, s.hq, s.hd, htap);
+    launch_gate_up(1, dim3(F / MOE_UNIT, S), st, L, x, 0, ids, nullptr, nullptr, nullptr, shared, 1, s.hq, s.hd, htap);
   }
   s.h_rows = htap ? (size_t)S : 0;
   s.last_F = F;
   {
     prof_scope pd(c, K_DOWN_DECODE, st);
-    hipLaunchKernelGGL(k_down_decode, dim3(H / 16), dim3(64 * S), lds2, st, L.m[T_DOWN].nib,
+    hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].nib,
                        reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc), s.hq, s.hd, ids, wts, k, E, S, F, H,
                        per_slot ? 1 : 0, out);
   }
@@ -597,8 +578,8 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   const int k = d.n_used, E = d.n_expert, P = T * k;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
   const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
-  const int nt_gu = pick_nt_gate_up(d.hidden), nt_dn = pick_nt_down(d.ffn);
-  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || !nt_gu || !nt_dn)
+  const int np_gu = pick_np(d.hidden, 4), np_dn = pick_np(d.ffn, 2);
+  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || !np_gu || !np_dn)
     return fail(c, MOE_ERR_UNSUPPORTED, "grouped: shape outside kernel range");
   scratch &s = c->sc;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *act = inv + P;
@@ -610,15 +591,15 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   const int ny = (P < E ? P : E) + shared;
   {
     prof_scope pg(c, K_GU_GROUPED, st);
-    launch_gate_up(nt_gu, dim3(d.ffn / MOE_RG, ny), st, L, x, 1, ids, offsets, perm, act, shared, T, s.hq, s.hd,
+    launch_gate_up(np_gu, dim3(d.ffn / MOE_UNIT, ny), st, L, x, 1, ids, offsets, perm, act, shared, T, s.hq, s.hd,
                    htap);
   }
   s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
   s.last_F = d.ffn;
   {
     prof_scope pd(c, K_DOWN_GROUPED, st);
-    launch_down(nt_dn, dim3(d.hidden / MOE_RG, ny), st, L, s.hq, s.hd, 1, ids, offsets, perm, act, wts, shared, T,
-                s.y);
+    launch_down_grp(np_dn, dim3(d.hidden / MOE_UNIT, ny), st, L, s.hq, s.hd, offsets, perm, act, wts, shared, T,
+                    s.y);
   }
   {
     prof_scope pc(c, K_COMBINE, st);
@@ -804,7 +785,7 @@ extern "C" moe_status moe_debug_quantize_q8_0(moe_ctx *c, const float *x, int n,
   if (!x || !qs || !d || n <= 0 || n % 32) return fail(c, MOE_ERR_INVALID_ARG, "moe_debug_quantize_q8_0: bad arguments");
   HIPC(c, hipSetDevice(c->device));
   const int nb = n / 32;
-  hipLaunchKernelGGL(k_debug_quantize, dim3(ceil_div(nb, 64)), dim3(64), 0, (hipStream_t)stream, x, nb, qs, d);
+  hipLaunchKernelGGL(k_debug_quantize, dim3(ceil_div(nb, 32)), dim3(64), 0, (hipStream_t)stream, x, nb, qs, d);
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
