@@ -5,13 +5,11 @@
 //
 // Weight layout in HBM (written by the repack/generator kernels, see
 // kernels_weights.h): rows in tiles of 16, the reduction dim in quads of
-// 4 blocks (128 weights); for every (tile, quad) the 64 lanes of a wave read
-// one contiguous KiB:
-//   nib[tile][q][l]      uint4  the 16 nibble bytes of block 4q + l/16 of
-//                               row 16*tile + l%16 (ggml's bytes, unchanged)
-//   sc [tile][q/4][l]    u32    byte q%4: that block's E8M0 exponent
-// which is exactly the A-operand lane layout of the 16x16x128 MFMA: lane
-// r + 16g holds row r, K-block g, nibble e at K offset e.  A ggml byte j holds
+// 4 blocks (128 weights), records of 4 quads; lane l of a wave reading quad
+// q of a tile gets the 16 nibble bytes of block 4q + l/16 of row l%16 (ggml's
+// bytes, unchanged), and one exponent dword per 4 quads (byte q%4).  That is
+// exactly the A-operand lane layout of the 16x16x128 MFMA: lane r + 16g
+// holds row r, K-block g, nibble e at K offset e.  A ggml byte j holds
 // element j (low nibble) and j+16 (high), so K offset e of a block carries
 // element sigma(e) = e/2 + 16*(e%2); the activations are laid out to match.
 //
@@ -39,6 +37,7 @@
 #pragma once
 
 #include "device_common.h"
+#include "kernels_weights.h"
 
 #define MOE_TILE 16     // rows per MFMA tile
 #define MOE_UNIT 32     // rows per h unit (one Q8_0 block of the SwiGLU output)
@@ -77,9 +76,12 @@ __device__ __forceinline__ float q_lo(float q) { return (float)(((int)q) & 15); 
 
 // Q8_0 of nb blocks of one f32 row (ggml's x86 rounding: d = fp16(amax/127),
 // q = rint(x * 127/amax)) into the staged format.
-__device__ __forceinline__ void stage_quant(const float *__restrict__ x, int nb, uint32_t *xs, float *dy, int lane) {
-  const int h = lane & 1;
-  for (int b = lane >> 1; b < nb; b += 32) {
+// tid / nthr: this thread's index among the nthr threads (a multiple of
+// 64, whole waves) that share the work.
+__device__ __forceinline__ void stage_quant(const float *__restrict__ x, int nb, uint32_t *xs, float *dy, int tid,
+                                            int nthr) {
+  const int h = tid & 1;
+  for (int b = tid >> 1; b < nb; b += nthr >> 1) {
     const float4 *xb = reinterpret_cast<const float4 *>(x + (size_t)b * MOE_QK + 8 * h);
     const float4 a0 = xb[0], a1 = xb[1], c0 = xb[4], c1 = xb[5];
     const float lo[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
@@ -201,34 +203,36 @@ struct wquad {
   u32x4_t w[NW];
 };
 
-// One weight stream: a (matrix, tile) pair as two buffer resources (base in
-// SGPRs, bounds-checked: a read past the tile returns 0), its nibble quads and
-// its exponent dwords.
+// One weight stream: a (matrix, tile) pair's records as a buffer resource
+// (base in SGPRs, bounds-checked: a read past the tile returns 0).
 struct wstream {
-  __amdgpu_buffer_rsrc_t nib, sc;
+  __amdgpu_buffer_rsrc_t rec;
 };
 
 #define MOE_RSRC_FLAGS 0x00020000  // raw buffer, 32-bit dwords, no swizzle
 #define MOE_CPOL_NT 2              // non-temporal loads: weights are read once per call
 
-__device__ __forceinline__ wstream make_wstream(const uint4 *nib, const uint32_t *sc, size_t tile, int NQ, int NQ4) {
-  wstream w;
-  w.nib = __builtin_amdgcn_make_buffer_rsrc((void *)(nib + tile * NQ * 64), 0, NQ * 1024, MOE_RSRC_FLAGS);
-  w.sc = __builtin_amdgcn_make_buffer_rsrc((void *)(sc + tile * NQ4 * 64), 0, NQ4 * 256, MOE_RSRC_FLAGS);
-  return w;
+// tile: index of the 16-row tile over all experts of the tensor.
+__device__ __forceinline__ wstream make_wstream(const uint8_t *w, size_t tile, int NG) {
+  wstream s;
+  s.rec = __builtin_amdgcn_make_buffer_rsrc((void *)(w + tile * NG * MOE_REC_BYTES), 0, NG * MOE_REC_BYTES,
+                                            MOE_RSRC_FLAGS);
+  return s;
 }
 
 template <int NW>
 __device__ __forceinline__ void load_wquad(wquad<NW> &b, const wstream (&ws)[NW], int q, int lane) {
 #pragma unroll
   for (int i = 0; i < NW; i++)
-    b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(ws[i].nib, lane * 16, q * 1024, MOE_CPOL_NT);
+    b.w[i] = __builtin_amdgcn_raw_buffer_load_b128(ws[i].rec, lane * 16, (q >> 2) * MOE_REC_BYTES + (q & 3) * 1024,
+                                                   MOE_CPOL_NT);
 }
 
 template <int NW>
 __device__ __forceinline__ void load_scales(uint32_t (&sc)[NW], const wstream (&ws)[NW], int g, int lane) {
 #pragma unroll
-  for (int i = 0; i < NW; i++) sc[i] = __builtin_amdgcn_raw_buffer_load_b32(ws[i].sc, lane * 4, g * 256, 0);
+  for (int i = 0; i < NW; i++)
+    sc[i] = __builtin_amdgcn_raw_buffer_load_b32(ws[i].rec, lane * 4, g * MOE_REC_BYTES + MOE_REC_SC, 0);
 }
 
 template <int SEL>
@@ -260,62 +264,135 @@ __device__ __forceinline__ void quad_mma(const wquad<NW> &b, const uint32_t (&sc
     for (int i = 0; i < NW; i++) asm volatile("" : "+v"(acc[p][i]));
 }
 
-template <int NW>
+// Load ring of D quads (D = 4 or 8): D - 1 quads in flight ahead of the one
+// being multiplied, and the exponent dwords of the D/4 groups the current
+// window of D quads spans.
+template <int NW, int D>
 struct kring {
-  wquad<NW> q[4];
-  uint32_t sc[NW];
+  static_assert(D == 4 || D == 8, "ring of 4 or 8 quads");
+  wquad<NW> q[D];
+  uint32_t sc[D / 4][NW];
 };
 
-// Issue the first 3 quads and the first exponent group (call before staging
-// the activations, so the weight loads overlap it).
-template <int NW>
-__device__ __forceinline__ void kloop_prime(kring<NW> &r, const wstream (&ws)[NW], int q0, int q1, int lane) {
+// Issue the first D - 1 quads and the first window's exponents (call before
+// staging the activations, so the weight loads overlap it).
+template <int NW, int D>
+__device__ __forceinline__ void kloop_prime(kring<NW, D> &r, const wstream (&ws)[NW], int q0, int q1, int lane) {
   if (q1 <= q0) return;
+  const int glast = (q1 - 1) >> 2;
 #pragma unroll
-  for (int d = 0; d < 3; d++) load_wquad<NW>(r.q[d], ws, q0 + d < q1 ? q0 + d : q1 - 1, lane);
-  load_scales<NW>(r.sc, ws, q0 >> 2, lane);
+  for (int d = 0; d < D - 1; d++) load_wquad<NW>(r.q[d], ws, q0 + d < q1 ? q0 + d : q1 - 1, lane);
+#pragma unroll
+  for (int g = 0; g < D / 4; g++) {
+    const int gg = (q0 >> 2) + g;
+    load_scales<NW>(r.sc[g], ws, gg < glast ? gg : glast, lane);
+  }
 }
 
-// K loop over quads [q0, q1).  The main loop covers whole groups of 4 quads
-// with no exit inside, and each quad's loads and math are pinned in order
-// (quad_mma's asm pins, the memory fence below), so the 4 ring slots keep
-// their registers across iterations: no copies at the back edge, which
-// would wait for every load in flight.  The last partial group is a
+// K loop over quads [q0, q1), q0 % 4 == 0.  The main loop covers whole
+// windows of D quads with no exit inside, and each quad's loads and math are
+// pinned in order (quad_mma's asm pins, the memory fence below), so the ring
+// slots keep their registers across iterations: no copies at the back edge,
+// which would wait for every load in flight.  The last partial window is a
 // guarded tail.
-template <int NW, int NP>
-__device__ __forceinline__ void kloop(kring<NW> &r, const wstream (&ws)[NW], int q0, int q1, const bsel (&bs)[NP],
-                                          const uint32_t *xs, const float *dy, int lane, f32x4_t (&acc)[NP][NW]) {
+template <int NW, int NP, int D>
+__device__ __forceinline__ void kloop(kring<NW, D> &r, const wstream (&ws)[NW], int q0, int q1, const bsel (&bs)[NP],
+                                      const uint32_t *xs, const float *dy, int lane, f32x4_t (&acc)[NP][NW]) {
 #pragma unroll
   for (int p = 0; p < NP; p++)
 #pragma unroll
     for (int i = 0; i < NW; i++) acc[p][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
   if (q1 <= q0) return;
   const int glast = (q1 - 1) >> 2;
-  uint32_t scn[NW];
-#define MOE_KSTEP(J)                                                    \
-  {                                                                     \
-    const int q = qb + J, qn = q + 3;                                   \
-    load_wquad<NW>(r.q[(J + 3) & 3], ws, qn < q1 ? qn : q1 - 1, lane);  \
-    asm volatile("" ::: "memory");     /* no hoisting of later loads */ \
-    __builtin_amdgcn_sched_barrier(0); /* keep the prefetch ahead */    \
-    quad_mma<J, NW, NP>(r.q[J], r.sc, q - q0, bs, xs, dy, acc);         \
+  uint32_t scn[D / 4][NW];
+#define MOE_KSTEP(J)                                                              \
+  {                                                                               \
+    const int q = qb + (J), qn = q + D - 1;                                       \
+    load_wquad<NW>(r.q[((J) + D - 1) % D], ws, qn < q1 ? qn : q1 - 1, lane);      \
+    asm volatile("" ::: "memory");     /* no hoisting of later loads */           \
+    __builtin_amdgcn_sched_barrier(0); /* keep the prefetch ahead */              \
+    quad_mma<(J) & 3, NW, NP>(r.q[J], r.sc[(J) / 4], q - q0, bs, xs, dy, acc);     \
   }
   int qb = q0;
-  for (; qb + 4 <= q1; qb += 4) {
-    const int gn = (qb >> 2) + 1;
-    load_scales<NW>(scn, ws, gn < glast ? gn : glast, lane);
-    MOE_KSTEP(0)
-    MOE_KSTEP(1)
-    MOE_KSTEP(2)
-    MOE_KSTEP(3)
+  for (; qb + D <= q1; qb += D) {
 #pragma unroll
-    for (int i = 0; i < NW; i++) r.sc[i] = scn[i];
+    for (int g = 0; g < D / 4; g++) {
+      const int gn = (qb >> 2) + D / 4 + g;
+      load_scales<NW>(scn[g], ws, gn < glast ? gn : glast, lane);
+    }
+    MOE_KSTEP(0) MOE_KSTEP(1) MOE_KSTEP(2) MOE_KSTEP(3)
+    if constexpr (D == 8) { MOE_KSTEP(4) MOE_KSTEP(5) MOE_KSTEP(6) MOE_KSTEP(7) }
+#pragma unroll
+    for (int g = 0; g < D / 4; g++)
+#pragma unroll
+      for (int i = 0; i < NW; i++) r.sc[g][i] = scn[g][i];
   }
-  // tail: 1-3 quads of the last group (their exponents are in r.sc)
+  // tail: fewer than D quads (their exponents are in r.sc)
   if (qb < q1) MOE_KSTEP(0)
   if (qb + 1 < q1) MOE_KSTEP(1)
   if (qb + 2 < q1) MOE_KSTEP(2)
+  if constexpr (D == 8) {
+    if (qb + 3 < q1) MOE_KSTEP(3)
+    if (qb + 4 < q1) MOE_KSTEP(4)
+    if (qb + 5 < q1) MOE_KSTEP(5)
+    if (qb + 6 < q1) MOE_KSTEP(6)
+  }
 #undef MOE_KSTEP
+}
+
+// The same loop for a compile-time number of quads NQW, fully unrolled:
+// straight-line code, so the compiler's wait counts are exact (in the
+// rolled loop it has to be conservative at the back edge and waits for more
+// of the ring than the quad about to be used).
+template <int NW, int NP, int D, int NQW>
+__device__ __forceinline__ void kloop_fixed(kring<NW, D> &r, const wstream (&ws)[NW], int q0, const bsel (&bs)[NP],
+                                            const uint32_t *xs, const float *dy, int lane, f32x4_t (&acc)[NP][NW]) {
+#pragma unroll
+  for (int p = 0; p < NP; p++)
+#pragma unroll
+    for (int i = 0; i < NW; i++) acc[p][i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  constexpr int NG = (NQW + 3) / 4;  // exponent groups of the chunk
+  uint32_t sc[NG][NW];
+  // the primed window's groups are in r.sc
+#pragma unroll
+  for (int g = 0; g < D / 4 && g < NG; g++)
+#pragma unroll
+    for (int i = 0; i < NW; i++) sc[g][i] = r.sc[g][i];
+#pragma unroll
+  for (int ql = 0; ql < NQW; ql++) {
+    const int J = ql % D;
+    if (J == 0) {
+      // exponents of the next window, one window ahead
+#pragma unroll
+      for (int g = 0; g < D / 4; g++) {
+        const int gn = ql / 4 + D / 4 + g;
+        if (gn < NG) load_scales<NW>(sc[gn], ws, (q0 >> 2) + gn, lane);
+      }
+    }
+    const int qn = ql + D - 1 < NQW ? ql + D - 1 : NQW - 1;
+    load_wquad<NW>(r.q[(J + D - 1) % D], ws, q0 + qn, lane);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    switch (ql & 3) {
+      case 0: quad_mma<0, NW, NP>(r.q[J], sc[ql >> 2], ql, bs, xs, dy, acc); break;
+      case 1: quad_mma<1, NW, NP>(r.q[J], sc[ql >> 2], ql, bs, xs, dy, acc); break;
+      case 2: quad_mma<2, NW, NP>(r.q[J], sc[ql >> 2], ql, bs, xs, dy, acc); break;
+      default: quad_mma<3, NW, NP>(r.q[J], sc[ql >> 2], ql, bs, xs, dy, acc); break;
+    }
+  }
+}
+
+// Dispatch on the wave's chunk length: the lengths the V3 and C1 shapes
+// produce run the unrolled loop, anything else the rolled one.
+template <int NW, int NP, int D>
+__device__ __forceinline__ void kloop_any(kring<NW, D> &r, const wstream (&ws)[NW], int q0, int q1,
+                                          const bsel (&bs)[NP], const uint32_t *xs, const float *dy, int lane,
+                                          f32x4_t (&acc)[NP][NW]) {
+  switch (q1 - q0) {
+    case 28: kloop_fixed<NW, NP, D, 28>(r, ws, q0, bs, xs, dy, lane, acc); break;
+    case 16: kloop_fixed<NW, NP, D, 16>(r, ws, q0, bs, xs, dy, lane, acc); break;
+    default: kloop<NW, NP, D>(r, ws, q0, q1, bs, xs, dy, lane, acc); break;
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -435,53 +512,55 @@ __host__ __device__ __forceinline__ int wave_blocks(int NQ, int NW) {
 }
 
 // gate/up -> clamp -> SwiGLU -> Q8_0(h).  One workgroup of 4 waves per
-// (32-row unit of F, expert column y).  The waves split the reduction dim;
-// each stages its part of the activations of a batch of up to 2*NP tokens,
-// streams its quads of the unit's 2 tiles of gate and up once per batch, and
-// the partial sums meet in LDS in wave order; then one wave per 2 tokens
-// applies clamp + SwiGLU and quantizes the unit's 32 h values (one Q8_0
-// block per token).  Decode (grouped == 0) is the same kernel with column
-// y = slot and one token.  grid (F/32, ny), 256 threads.
-// LDS: per wave [zero 4][xs 2NP*NBW*16][dy 2NP*NBW] dwords, reused for the
-// partials [wave][4 streams][2NP][16] after the K loops.
-// NP == 1 (decode and small batches) is held to 3 waves per SIMD, so a
-// V3 decode's 576 workgroups are resident at once (3 per CU).
+// (32-row unit of F, expert column y): wave w streams tile w%2 of the unit
+// (gate and up) over K-half w/2 (whole groups of 4 quads), against the
+// activations of a batch of up to 2*NP tokens, which the two waves of each
+// K-half quantize into a shared LDS region.  The K-halves meet in LDS in
+// order; then one wave per 2 tokens applies clamp + SwiGLU and quantizes the
+// unit's 32 h values (one Q8_0 block per token).  Decode (grouped == 0) is
+// the same kernel with column y = slot and one token.
+// grid (F/32, ny), 256 threads.  LDS: per K-half [zero 4][xs 2NP*NBW*16]
+// [dy 2NP*NBW] dwords, reused for the partials [wave][2 streams][2NP][16].
+// NP == 1 (decode and small batches) is held to 3 waves per SIMD, so a V3
+// decode's 576 workgroups are resident at once (3 per CU).
+#define MOE_GU_KS 2    // K parts of the gate/up workgroup (x 2 tiles = 4 waves)
+#define MOE_GU_RING 4  // quads in a gate/up wave's load ring
+
 template <int NP>
-__global__ __launch_bounds__(64 * MOE_GRP_WAVES) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 3 : (NP == 2 ? 2 : 1))))
+__global__ __launch_bounds__(64 * 2 * MOE_GU_KS) __attribute__((amdgpu_waves_per_eu(NP == 1 ? 3 : (NP == 2 ? 2 : 1))))
 void k_gate_up(
-    const uint4 *__restrict__ nib_g, const uint4 *__restrict__ nib_u, const uint32_t *__restrict__ sc_g,
-    const uint32_t *__restrict__ sc_u, const float *__restrict__ x, int grouped, const int32_t *__restrict__ ids,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm, const int32_t *__restrict__ act, int k,
-    int E, int shared, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
-    float *__restrict__ htap) {
+    const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const float *__restrict__ x, int grouped,
+    const int32_t *__restrict__ ids, const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm,
+    const int32_t *__restrict__ act, int k, int E, int shared, int T, int F, int H, float clamp,
+    uint32_t *__restrict__ hs, float *__restrict__ hd, float *__restrict__ htap) {
   extern __shared__ __align__(16) uint32_t lds[];
   constexpr int NTOK = 2 * NP;
   const int NQ = H / 128, NQ4 = moe_nq4(NQ), U = F / MOE_UNIT, tiles = F / MOE_TILE;
-  const int NBW = wave_blocks(NQ, MOE_GRP_WAVES);
-  const int wave_words = 4 + NTOK * NBW * (MOE_XSW + 1);
+  const int NBW = wave_blocks(NQ, MOE_GU_KS);
+  const int part_words = 4 + NTOK * NBW * (MOE_XSW + 1);
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ti = wave & 1, kp = wave >> 1;
   const int P = T * k;
   const unit_t un = unit_of(blockIdx.y, gridDim.y, grouped, ids, offsets, act, k, E, shared, P, T);
   if (grouped && !un.valid) return;
   const int u = blockIdx.x;
   int q0, q1;
-  wave_quads(NQ, MOE_GRP_WAVES, wave, q0, q1);
+  wave_quads(NQ, MOE_GU_KS, kp, q0, q1);
   const int nb = 4 * (q1 - q0);
-  uint32_t *xs = lds + (size_t)wave * wave_words;
+  uint32_t *xs = lds + (size_t)kp * part_words;
   float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)NTOK * NBW * MOE_XSW);
-  float *red = reinterpret_cast<float *>(lds);  // [wave][4 streams][NTOK][16], after the K loops
-  const size_t t0 = (size_t)un.mat * tiles + 2 * u;
-  const wstream ws[4] = {make_wstream(nib_g, sc_g, t0, NQ, NQ4), make_wstream(nib_g, sc_g, t0 + 1, NQ, NQ4),
-                         make_wstream(nib_u, sc_u, t0, NQ, NQ4), make_wstream(nib_u, sc_u, t0 + 1, NQ, NQ4)};
+  float *red = reinterpret_cast<float *>(lds);  // [wave][2 streams][NTOK][16], after the K loops
+  const size_t t0 = (size_t)un.mat * tiles + 2 * u + ti;
+  const wstream ws[2] = {make_wstream(w_g, t0, NQ4), make_wstream(w_u, t0, NQ4)};
   for (int i0 = 0; i0 < un.nrows; i0 += NTOK) {
     const int nt = un.nrows - i0 < NTOK ? un.nrows - i0 : NTOK;
-    kring<4> ring;
-    kloop_prime<4>(ring, ws, q0, q1, lane);
-    if (lane < 4) xs[lane] = 0u;
+    kring<2, MOE_GU_RING> ring;
+    kloop_prime<2, MOE_GU_RING>(ring, ws, q0, q1, lane);
+    if (ti == 0 && lane < 4) xs[lane] = 0u;
     for (int t = 0; t < nt; t++) {
       const int tok = grouped ? token_of(un, un.row0 + i0 + t, perm, k, P) : 0;
       stage_quant(x + (size_t)tok * H + (size_t)q0 * 128, nb, xs + 4 + (size_t)t * NBW * MOE_XSW,
-                  dy + (size_t)t * NBW, lane);
+                  dy + (size_t)t * NBW, lane + 64 * ti, 128);
     }
     __syncthreads();
     bsel bs[NP];
@@ -489,30 +568,31 @@ void k_gate_up(
     for (int p = 0; p < NP; p++)
       bs[p] = make_bsel(lane, 4 + 2 * p * NBW * MOE_XSW, 4 + (2 * p + 1) * NBW * MOE_XSW, 2 * p * NBW,
                         (2 * p + 1) * NBW, 2 * p < nt, 2 * p + 1 < nt, 0);
-    f32x4_t acc[NP][4];
-    kloop<4, NP>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
-    __syncthreads();  // every wave is done with its staged rows before red overwrites them
+    f32x4_t acc[NP][2];
+    kloop_any<2, NP, MOE_GU_RING>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
+    __syncthreads();  // every wave is done with the staged rows before red overwrites them
     const int gb = lane >> 4, tp = (lane >> 3) & 1;
 #pragma unroll
     for (int p = 0; p < NP; p++)
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 2; i++)
 #pragma unroll
         for (int r = 0; r < 4; r++) {
           const float v = col8_sum(acc[p][i][r]);
-          if ((lane & 7) == 0) red[((wave * 4 + i) * NTOK + 2 * p + tp) * MOE_TILE + 4 * gb + r] = v;
+          if ((lane & 7) == 0) red[((wave * 2 + i) * NTOK + 2 * p + tp) * MOE_TILE + 4 * gb + r] = v;
         }
     __syncthreads();
     // epilogue: wave w takes token slots 2w, 2w+1 (lane half = token, lane j = row)
-    for (int t = 2 * wave; t < nt; t += 2 * MOE_GRP_WAVES) {
+    for (int t = 2 * wave; t < nt; t += 4 * MOE_GU_KS) {
       const int ts = t + (lane >> 5);
-      const int j = lane & 31, ti = j >> 4, rr = j & 15;
+      const int j = lane & 31, tj = j >> 4, rr = j & 15;
       const bool live = ts < nt;
       float gsum = 0.0f, usum = 0.0f;
       if (live)
-        for (int w = 0; w < MOE_GRP_WAVES; w++) {
-          gsum += red[((w * 4 + ti) * NTOK + ts) * MOE_TILE + rr];
-          usum += red[((w * 4 + 2 + ti) * NTOK + ts) * MOE_TILE + rr];
+        for (int q = 0; q < MOE_GU_KS; q++) {
+          const int w = tj + 2 * q;  // the wave of tile tj, K part q
+          gsum += red[((w * 2 + 0) * NTOK + ts) * MOE_TILE + rr];
+          usum += red[((w * 2 + 1) * NTOK + ts) * MOE_TILE + rr];
         }
       const float h = live && un.valid ? swiglu(gsum, usum, clamp) : 0.0f;
       const int hrow = un.row0 + i0 + (live ? ts : 0);
@@ -533,8 +613,8 @@ void k_gate_up(
 // grid H/16, 64*S threads.  LDS: per wave [zero 4][xs F/32*16][dy F/32]
 // dwords, then ys[S][16].
 __global__ __launch_bounds__(1024) void k_down_dec(
-    const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hs,
-    const float *__restrict__ hd, const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int E,
+    const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+    const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int E,
     int S, int F, int H, int per_slot, float *__restrict__ out) {
   extern __shared__ __align__(16) uint32_t lds[];
   const int NQ = F / 128, NQ4 = moe_nq4(NQ), tiles = H / MOE_TILE, U = F / MOE_UNIT;
@@ -544,9 +624,9 @@ __global__ __launch_bounds__(1024) void k_down_dec(
   int e = s < k ? ids[s] : E;
   const bool valid = s >= k || (unsigned)e < (unsigned)E;  // an out-of-range id reads nothing, yields 0
   e = valid ? e : 0;
-  const wstream ws[1] = {make_wstream(nib_d, sc_d, (size_t)e * tiles + tile, NQ, NQ4)};
-  kring<1> ring;
-  kloop_prime<1>(ring, ws, 0, NQ, lane);
+  const wstream ws[1] = {make_wstream(w_d, (size_t)e * tiles + tile, NQ4)};
+  kring<1, 4> ring;
+  kloop_prime<1, 4>(ring, ws, 0, NQ, lane);
   uint32_t *xs = lds + (size_t)s * wave_words;
   float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)nb * MOE_XSW);
   float *ys = reinterpret_cast<float *>(lds + (size_t)S * wave_words);  // [S][16]
@@ -555,7 +635,7 @@ __global__ __launch_bounds__(1024) void k_down_dec(
   __syncthreads();
   const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
   f32x4_t acc[1][1];
-  kloop<1, 1>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
+  kloop_any<1, 1, 4>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
   const int gb = lane >> 4;
   const float wt = s < k ? wts[s] : 1.0f;
   float v[4];
@@ -589,8 +669,8 @@ __global__ __launch_bounds__(1024) void k_down_dec(
 // grid (H/32, ny), 256 threads.
 template <int NP>
 __global__ __launch_bounds__(64 * MOE_GRP_WAVES) void k_down_grp(
-    const uint4 *__restrict__ nib_d, const uint32_t *__restrict__ sc_d, const uint32_t *__restrict__ hs,
-    const float *__restrict__ hd, const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm,
+    const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+    const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm,
     const int32_t *__restrict__ act, const float *__restrict__ wts, int k, int E, int shared, int T, int F, int H,
     float *__restrict__ y) {
   extern __shared__ __align__(16) uint32_t lds[];
@@ -610,11 +690,11 @@ __global__ __launch_bounds__(64 * MOE_GRP_WAVES) void k_down_grp(
   float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)NTOK * NBW * MOE_XSW);
   float *red = reinterpret_cast<float *>(lds);  // [wave][2 tiles][NTOK][16]
   const size_t t0 = (size_t)un.mat * tiles + 2 * u;
-  const wstream ws[2] = {make_wstream(nib_d, sc_d, t0, NQ, NQ4), make_wstream(nib_d, sc_d, t0 + 1, NQ, NQ4)};
+  const wstream ws[2] = {make_wstream(w_d, t0, NQ4), make_wstream(w_d, t0 + 1, NQ4)};
   for (int i0 = 0; i0 < un.nrows; i0 += NTOK) {
     const int nt = un.nrows - i0 < NTOK ? un.nrows - i0 : NTOK;
-    kring<2> ring;
-    kloop_prime<2>(ring, ws, q0, q1, lane);
+    kring<2, 4> ring;
+    kloop_prime<2, 4>(ring, ws, q0, q1, lane);
     if (lane < 4) xs[lane] = 0u;
     for (int t = 0; t < nt; t++) {
       const size_t hrow = (size_t)(un.row0 + i0 + t);
@@ -628,7 +708,7 @@ __global__ __launch_bounds__(64 * MOE_GRP_WAVES) void k_down_grp(
       bs[p] = make_bsel(lane, 4 + 2 * p * NBW * MOE_XSW, 4 + (2 * p + 1) * NBW * MOE_XSW, 2 * p * NBW,
                         (2 * p + 1) * NBW, 2 * p < nt, 2 * p + 1 < nt, 0);
     f32x4_t acc[NP][2];
-    kloop<2, NP>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
+    kloop<2, NP, 4>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
     __syncthreads();
     const int gb = lane >> 4, tp = (lane >> 3) & 1;
 #pragma unroll
@@ -655,6 +735,12 @@ __global__ __launch_bounds__(64 * MOE_GRP_WAVES) void k_down_grp(
 }
 
 // LDS bytes of the kernels.
+static inline size_t gate_up_lds_bytes(int H, int NP) {
+  const int NBW = wave_blocks(H / 128, MOE_GU_KS);
+  const size_t stage = ((size_t)4 + (size_t)2 * NP * NBW * (MOE_XSW + 1)) * 4 * MOE_GU_KS;
+  const size_t red = (size_t)4 * 2 * 2 * NP * MOE_TILE * 4;
+  return stage > red ? stage : red;
+}
 static inline size_t grp_lds_bytes(int K, int NP, int streams) {
   const int NBW = wave_blocks(K / 128, MOE_GRP_WAVES);
   const size_t stage = ((size_t)4 + (size_t)2 * NP * NBW * (MOE_XSW + 1)) * 4 * MOE_GRP_WAVES;
@@ -677,7 +763,7 @@ __global__ __launch_bounds__(64) void k_debug_quantize(const float *__restrict__
   const int lane = threadIdx.x;
   const int b0 = blockIdx.x * 32;
   const int nb = n_blocks - b0 < 32 ? n_blocks - b0 : 32;
-  stage_quant(x + (size_t)b0 * MOE_QK, nb, xs, dy, lane);
+  stage_quant(x + (size_t)b0 * MOE_QK, nb, xs, dy, lane, 64);
   __syncthreads();
   for (int i = lane; i < nb * 32; i += 64) {
     const int b = i >> 5, e = i & 31;  // MFMA K offset e of block b

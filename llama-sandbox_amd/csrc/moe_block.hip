@@ -30,10 +30,9 @@ enum { T_GATE = 0, T_UP = 1, T_DOWN = 2 };
 // One tensor of a layer (gate, up or down) for all E' = E + has_shared
 // experts, in the row-interleaved layout of kernels_weights.h.
 struct dev_mat {
-  uint4 *nib = nullptr;   // E'*R*KB 16-byte nibble payloads
-  uint8_t *sc = nullptr;  // E' exponent planes of sc_per_exp bytes
+  uint8_t *w = nullptr;   // E' matrices of `stride` bytes (kernels_weights.h records)
   int rows = 0, kb = 0;
-  uint64_t sc_per_exp = 0;
+  uint64_t stride = 0;
 };
 
 struct dev_layer {
@@ -258,10 +257,8 @@ extern "C" void moe_ctx_destroy(moe_ctx *c) {
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
   for (auto &kv : c->layers)
-    for (dev_mat &m : kv.second.m) {
-      if (m.nib) (void)hipFree(m.nib);
-      if (m.sc) (void)hipFree(m.sc);
-    }
+    for (dev_mat &m : kv.second.m)
+      if (m.w) (void)hipFree(m.w);
   scratch_free(c->sc);
   for (auto &r : c->prof.pending) {
     (void)hipEventDestroy(r.a);
@@ -315,17 +312,12 @@ static moe_status layer_alloc(moe_ctx *c, int layer, const moe_layer_desc *d, de
   const int rows[3] = {d->ffn, d->ffn, d->hidden};
   const int kbs[3] = {d->hidden / 32, d->hidden / 32, d->ffn / 32};
   for (int t = 0; t < 3; t++) {
-    const size_t nb = (size_t)L.n_mats * rows[t] * kbs[t];
     L.m[t].rows = rows[t];
     L.m[t].kb = kbs[t];
-    L.m[t].sc_per_exp = sc_plane_bytes(rows[t], kbs[t]);
-    hipError_t e1 = hipMalloc(&L.m[t].nib, nb * 16);
-    hipError_t e2 = e1 == hipSuccess ? hipMalloc(&L.m[t].sc, (size_t)L.n_mats * L.m[t].sc_per_exp) : e1;
-    if (e1 != hipSuccess || e2 != hipSuccess) {
-      for (dev_mat &m : L.m) {
-        if (m.nib) (void)hipFree(m.nib);
-        if (m.sc) (void)hipFree(m.sc);
-      }
+    L.m[t].stride = mat_bytes(rows[t], kbs[t]);
+    if (hipMalloc(&L.m[t].w, (size_t)L.n_mats * L.m[t].stride) != hipSuccess) {
+      for (dev_mat &m : L.m)
+        if (m.w) (void)hipFree(m.w);
       (void)hipGetLastError();
       return fail(c, MOE_ERR_OUT_OF_BUDGET, "layer %d: device allocation failed; CPU fallback", layer);
     }
@@ -340,10 +332,8 @@ static moe_status layer_alloc(moe_ctx *c, int layer, const moe_layer_desc *d, de
 static void layer_drop(moe_ctx *c, int layer) {
   auto it = c->layers.find(layer);
   if (it == c->layers.end()) return;
-  for (dev_mat &m : it->second.m) {
-    if (m.nib) (void)hipFree(m.nib);
-    if (m.sc) (void)hipFree(m.sc);
-  }
+  for (dev_mat &m : it->second.m)
+    if (m.w) (void)hipFree(m.w);
   c->used -= it->second.bytes;
   c->layers.erase(it);
 }
@@ -378,7 +368,6 @@ extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_de
     for (int part = 0; part < 1 + d->has_shared && st == MOE_OK; part++) {
       const uint8_t *host = (const uint8_t *)src[t][part];
       const size_t n_exp = part == 0 ? (size_t)d->n_expert : 1;
-      const size_t base = part == 0 ? 0 : per_exp * d->n_expert;
       for (size_t e0 = 0; e0 < n_exp; e0 += batch) {
         const size_t ne = n_exp - e0 < batch ? n_exp - e0 : batch;
         const size_t n = ne * per_exp, off = e0 * per_exp;
@@ -388,7 +377,7 @@ extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_de
         }
         const size_t first = (part == 0 ? e0 : (size_t)d->n_expert);  // expert index of the batch's first matrix
         hipLaunchKernelGGL(k_repack_blocks, dim3(ceil_div((long)n, 256)), dim3(256), 0, 0, stage, (uint64_t)n,
-                           (uint64_t)per_exp, m.sc_per_exp, m.kb, m.nib + base + off, m.sc + first * m.sc_per_exp);
+                           (uint64_t)per_exp, m.stride, m.kb, m.w + first * m.stride);
       }
     }
   }
@@ -417,8 +406,7 @@ extern "C" moe_status moe_layer_generate(moe_ctx *c, int layer, const moe_layer_
                           (uint64_t)(uint32_t)expert;
       const uint64_t key = host_mix64(seed ^ host_mix64(id));
       hipLaunchKernelGGL(k_generate_blocks, dim3(ceil_div((long)per_exp, 256)), dim3(256), 0, 0, key,
-                         (uint64_t)per_exp, m.kb, (uint32_t)e_lo, (uint32_t)e_span, m.nib + per_exp * e,
-                         m.sc + m.sc_per_exp * e);
+                         (uint64_t)per_exp, m.kb, (uint32_t)e_lo, (uint32_t)e_span, m.w + m.stride * e);
     }
   }
   if (hipDeviceSynchronize() != hipSuccess) {
@@ -440,8 +428,8 @@ extern "C" moe_status moe_layer_read_blocks(moe_ctx *c, int layer, int tensor, i
   const size_t nb = (size_t)m.rows * m.kb;
   uint8_t *tmp = nullptr;
   HIPC(c, hipMalloc(&tmp, nb * 17));
-  hipLaunchKernelGGL(k_unpack_blocks, dim3(ceil_div((long)nb, 256)), dim3(256), 0, 0, m.nib + nb * expert,
-                     m.sc + m.sc_per_exp * expert, (uint64_t)nb, m.kb, tmp);
+  hipLaunchKernelGGL(k_unpack_blocks, dim3(ceil_div((long)nb, 256)), dim3(256), 0, 0, m.w + m.stride * expert,
+                     (uint64_t)nb, m.kb, tmp);
   hipError_t e = hipMemcpy(out, tmp, nb * 17, hipMemcpyDeviceToHost);
   (void)hipFree(tmp);
   if (e != hipSuccess) return fail(c, MOE_ERR_HIP, "moe_layer_read_blocks: copy failed");
@@ -507,18 +495,21 @@ static int pick_np(int K, int streams) {
   if (grp_lds_bytes(K, 2, streams) <= 65536) return 2;
   return grp_lds_bytes(K, 1, streams) <= 65536 ? 1 : 0;
 }
+static int pick_np_gate_up(int H) {
+  if (gate_up_lds_bytes(H, 4) <= 65536) return 4;
+  if (gate_up_lds_bytes(H, 2) <= 65536) return 2;
+  return gate_up_lds_bytes(H, 1) <= 65536 ? 1 : 0;
+}
 
 // gate/up launch; grouped == 0: decode, columns are slots (ids), one token.
 static void launch_gate_up(int NP, dim3 g, hipStream_t st, const dev_layer &L, const float *x, int grouped,
                            const int32_t *ids, const int32_t *offsets, const int32_t *perm, const int32_t *act,
                            int shared, int T, uint32_t *hq, float *hd, float *htap) {
   const moe_layer_desc &d = L.d;
-  const size_t lds = grp_lds_bytes(d.hidden, NP, 4);
-  const uint32_t *scg = reinterpret_cast<const uint32_t *>(L.m[T_GATE].sc);
-  const uint32_t *scu = reinterpret_cast<const uint32_t *>(L.m[T_UP].sc);
-#define MOE_GU_ARGS L.m[T_GATE].nib, L.m[T_UP].nib, scg, scu, x, grouped, ids, offsets, perm, act, d.n_used, \
+  const size_t lds = gate_up_lds_bytes(d.hidden, NP);
+#define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, x, grouped, ids, offsets, perm, act, d.n_used, \
                     d.n_expert, shared, T, d.ffn, d.hidden, d.clamp, hq, hd, htap
-  const dim3 blk(64 * MOE_GRP_WAVES);
+  const dim3 blk(64 * 2 * MOE_GU_KS);
   if (NP == 4) hipLaunchKernelGGL(k_gate_up<4>, g, blk, lds, st, MOE_GU_ARGS);
   else if (NP == 2) hipLaunchKernelGGL(k_gate_up<2>, g, blk, lds, st, MOE_GU_ARGS);
   else hipLaunchKernelGGL(k_gate_up<1>, g, blk, lds, st, MOE_GU_ARGS);
@@ -530,8 +521,7 @@ static void launch_down_grp(int NP, dim3 g, hipStream_t st, const dev_layer &L, 
                             int shared, int T, float *y) {
   const moe_layer_desc &d = L.d;
   const size_t lds = grp_lds_bytes(d.ffn, NP, 2);
-  const uint32_t *scd = reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc);
-#define MOE_DN_ARGS L.m[T_DOWN].nib, scd, hq, hd, offsets, perm, act, wts, d.n_used, d.n_expert, shared, T, d.ffn, \
+#define MOE_DN_ARGS L.m[T_DOWN].w, hq, hd, offsets, perm, act, wts, d.n_used, d.n_expert, shared, T, d.ffn, \
                     d.hidden, y
   const dim3 blk(64 * MOE_GRP_WAVES);
   if (NP == 4) hipLaunchKernelGGL(k_down_grp<4>, g, blk, lds, st, MOE_DN_ARGS);
@@ -552,7 +542,7 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   const int S = k + shared;
   scratch &s = c->sc;
   float *htap = c->taps ? s.htap : nullptr;
-  const size_t lds1 = grp_lds_bytes(H, 1, 4), lds2 = down_dec_lds_bytes(F, S);
+  const size_t lds1 = gate_up_lds_bytes(H, 1), lds2 = down_dec_lds_bytes(F, S);
   if (S > 16 || lds1 > 65536 || lds2 > 65536)
     return fail(c, MOE_ERR_UNSUPPORTED, "decode: more than 16 slots, or hidden/ffn too large");
   {
@@ -563,8 +553,8 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   s.last_F = F;
   {
     prof_scope pd(c, K_DOWN_DECODE, st);
-    hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].nib,
-                       reinterpret_cast<const uint32_t *>(L.m[T_DOWN].sc), s.hq, s.hd, ids, wts, k, E, S, F, H,
+    hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].w, s.hq, s.hd, ids,
+                       wts, k, E, S, F, H,
                        per_slot ? 1 : 0, out);
   }
   HIPC(c, hipGetLastError());
@@ -578,7 +568,7 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   const int k = d.n_used, E = d.n_expert, P = T * k;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
   const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
-  const int np_gu = pick_np(d.hidden, 4), np_dn = pick_np(d.ffn, 2);
+  const int np_gu = pick_np_gate_up(d.hidden), np_dn = pick_np(d.ffn, 2);
   if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || !np_gu || !np_dn)
     return fail(c, MOE_ERR_UNSUPPORTED, "grouped: shape outside kernel range");
   scratch &s = c->sc;
