@@ -530,6 +530,9 @@ static void launch_down_grp(int NP, dim3 g, hipStream_t st, const dev_layer &L, 
 #undef MOE_DN_ARGS
 }
 
+static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
+                                  int T, float *out, uint32_t flags, hipStream_t st);
+
 // The decode chain for T == 1, two launches: gate/up per (32-row unit, slot)
 // with SwiGLU and Q8_0 of h, then down per 16-row tile of H with one wave per
 // slot, the router weights and the slot-order combine.
@@ -544,7 +547,7 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   float *htap = c->taps ? s.htap : nullptr;
   const size_t lds1 = gate_up_lds_bytes(H, 1), lds2 = down_dec_lds_bytes(F, S);
   if (S > 16 || lds1 > 65536 || lds2 > 65536)
-    return fail(c, MOE_ERR_UNSUPPORTED, "decode: more than 16 slots, or hidden/ffn too large");
+    return forward_grouped(c, L, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
   {
     prof_scope pg(c, K_GU_DECODE, st);
     launch_gate_up(1, dim3(F / MOE_UNIT, S), st, L, x, 0, ids, nullptr, nullptr, nullptr, shared, 1, s.hq, s.hd, htap);
