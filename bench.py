@@ -51,6 +51,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cpus))")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the hipGraph")
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+                    help="c2 (default): the headline V3 decode line; c1/c3/c4/c5: one line per measured case of "
+                         "that configuration (C1 decode, C3 T=4/16/64 Zipf, C4 T=512 uniform and Zipf, C5 40-layer "
+                         "graph)")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB three times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
@@ -123,6 +127,183 @@ def cpu_baseline(seconds: float, threads: int, seed: int):
                       f"oracle/libmoe_oracle.so on {threads} threads, median per token",
             "gbps": round(touched / med / 1e3, 2)}
 
+MFMA_FP4_PEAK_TFLOPS = 10100.0  # MI355X dense MXFP4 MFMA, vendor figure
+
+
+def bench_config(args):
+    """The other configurations, one JSON line per measured case.
+
+    C1, C3, C4: a step is one moe_forward of T tokens on one resident layer;
+    the steps cycle over --layers layers (C1: 4, the rest: 8, so the touched
+    experts of consecutive steps are cold), each step with its own
+    activations and router logits (routed on the device before the timed
+    region), replayed as one hipGraph.  C5: 40 resident V3 layers, each with
+    its own token and routing, captured as ONE hipGraph of 40 layer calls
+    and replayed --steps times (default 256); a step is the 40-layer pass.
+    Bytes are the algorithmic ones: (distinct routed experts of the step +
+    shared) x 23,396,352 B per V3 expert, from the step's own ids."""
+    import numpy as np
+    import torch
+
+    import moe_block as mb
+    import workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    name = args.workload.upper()
+    cfg = wl.CONFIGS[name]
+    sh = cfg["shape"]
+    blk = mb.MoeBlock(0)
+    stream = torch.cuda.current_stream()
+
+    if name == "C5":
+        NL = cfg["layers"]
+        steps = args.steps
+        t0 = time.time()
+        for layer in range(NL):
+            blk.generate_layer(layer, sh, seed=args.seed + layer)
+        torch.cuda.synchronize()
+        log(f"generated {NL} V3 layers ({NL * sh.layer_bytes / 1e9:.1f} GB resident) in {time.time() - t0:.1f}s")
+        x_np, lg_np = wl.make_inputs(sh, NL, args.seed + 7)
+        x = torch.from_numpy(x_np).to(dev)
+        logits = torch.from_numpy(lg_np).to(dev)
+        ids = torch.empty((NL, sh.n_used), dtype=torch.int32, device=dev)
+        wts = torch.empty((NL, sh.n_used), dtype=torch.float32, device=dev)
+        blk.route(logits, sh.n_used, sh.route_mode, sh.norm, sh.scale, ids, wts)
+        out = torch.empty((NL, sh.hidden), dtype=torch.float32, device=dev)
+        blk.reserve(sh, 1)
+        torch.cuda.synchronize()
+        ids_np = ids.cpu().numpy()
+        step_bytes = float(sum(sh.touched_bytes(ids_np[i:i + 1]) for i in range(NL)))
+        g = blk.graph_capture(list(range(NL)), [x[i:i + 1] for i in range(NL)], [ids[i:i + 1] for i in range(NL)],
+                              [wts[i:i + 1] for i in range(NL)], [out[i:i + 1] for i in range(NL)])
+        for _ in range(max(1, args.warmup // 8)):
+            g.launch()
+        torch.cuda.synchronize()
+        ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t_a = time.perf_counter()
+        ev0.record(stream)
+        for _ in range(steps):
+            g.launch()
+        ev1.record(stream)
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t_a
+        ref = out.clone()
+        # eager pass of the same 40 layers with per-kernel events: kernel time per layer
+        blk.prof_enable(True)
+        blk.prof_read(reset=True)
+        for _ in range(8):
+            for i in range(NL):
+                blk.forward(i, x[i:i + 1], ids[i:i + 1], wts[i:i + 1], out[i:i + 1])
+        torch.cuda.synchronize()
+        stats = blk.prof_read(reset=True)
+        blk.prof_enable(False)
+        if not torch.equal(out.view(torch.int32), ref.view(torch.int32)):
+            raise SystemExit("bench: eager and graph outputs differ")
+        kern_us_layer = sum(v[1] for v in stats.values()) / (8 * NL)
+        us_step = elapsed / steps * 1e6
+        gbps = step_bytes * steps / elapsed / 1e9
+        line = {
+            "metric": "40-layer V3 decode step (one hipGraph), us/step + sustained HBM GB/s",
+            "value": round(us_step, 2), "unit": "us/step", "n_gpus": 1, "steps": steps,
+            "higher_is_better": False, "dtype": "mxfp4 x q8_0, f32 accumulate", "data": "synthetic",
+            "config": {"workload": f"C5: {NL} resident V3 layers ({NL * sh.layer_bytes / 1e9:.1f} GB), T=1, "
+                                   f"independent top-8 routing per layer, one hipGraph of {NL} layer calls "
+                                   f"replayed {steps} times"},
+            "us_per_layer": round(us_step / NL, 3),
+            "kernel_us_per_layer": round(kern_us_layer, 3),
+            "launch_overhead_us_per_layer": round(us_step / NL - kern_us_layer, 3),
+            "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "algorithmic_bytes_per_step": round(step_bytes),
+            "tokens_per_s": round(1e6 / us_step, 1),
+        }
+        log(f"C5: {us_step:.1f} us/step, {us_step / NL:.2f} us/layer (kernels {kern_us_layer:.2f}), "
+            f"{gbps:.0f} GB/s")
+        print(json.dumps(line), flush=True)
+        blk.close()
+        return
+
+    NL = args.layers if args.layers != 8 or name != "C1" else 4
+    steps, W = args.steps, args.warmup
+    if name == "C4" and steps == 256:
+        steps, W = 16, 4  # defaults sized for T=512
+    elif name == "C3" and steps == 256:
+        steps, W = 64, 8
+    t0 = time.time()
+    for layer in range(NL):
+        blk.generate_layer(layer, sh, seed=args.seed + layer)
+    torch.cuda.synchronize()
+    log(f"generated {NL} layers ({NL * sh.layer_bytes / 1e9:.2f} GB resident) in {time.time() - t0:.1f}s")
+    cases = [(T, z) for T in cfg["tokens"] for z in ((False, True) if cfg["zipf"] is None else (cfg["zipf"],))]
+    for T, zipf in cases:
+        n = W + steps
+        x_np, lg_np = wl.make_inputs(sh, n * T, args.seed + 11 * T + int(zipf), zipf=zipf)
+        x = torch.from_numpy(x_np).to(dev).view(n, T, sh.hidden)
+        logits = torch.from_numpy(lg_np).to(dev)
+        ids = torch.empty((n * T, sh.n_used), dtype=torch.int32, device=dev)
+        wts = torch.empty((n * T, sh.n_used), dtype=torch.float32, device=dev)
+        blk.route(logits, sh.n_used, sh.route_mode, sh.norm, sh.scale, ids, wts)
+        ids, wts = ids.view(n, T, sh.n_used), wts.view(n, T, sh.n_used)
+        out = torch.empty((n, T, sh.hidden), dtype=torch.float32, device=dev)
+        blk.reserve(sh, T)
+        torch.cuda.synchronize()
+        ids_np = ids.cpu().numpy()
+        touched = np.array([sh.touched_bytes(ids_np[i]) for i in range(n)], np.float64)
+        distinct = np.array([len(np.unique(ids_np[i])) for i in range(n)], np.float64)
+        hot = np.array([np.bincount(ids_np[i].ravel(), minlength=sh.n_expert).max() for i in range(n)])
+        layer_of = [i % NL for i in range(n)]
+        mk = lambda t, lo, hi: [t[i] for i in range(lo, hi)]  # noqa: E731
+        gw = blk.graph_capture(layer_of[:W], mk(x, 0, W), mk(ids, 0, W), mk(wts, 0, W), mk(out, 0, W)) if W else None
+        gk = blk.graph_capture(layer_of[W:n], mk(x, W, n), mk(ids, W, n), mk(wts, W, n), mk(out, W, n))
+        if gw is not None:
+            gw.launch()
+        torch.cuda.synchronize()
+        t_a = time.perf_counter()
+        gk.launch()
+        torch.cuda.synchronize()
+        elapsed = time.perf_counter() - t_a
+        ref = out[W:n].clone()
+        blk.prof_enable(True)
+        blk.prof_read(reset=True)
+        for i in range(W, n):
+            blk.forward(layer_of[i], x[i], ids[i], wts[i], out[i])
+        torch.cuda.synchronize()
+        stats = blk.prof_read(reset=True)
+        blk.prof_enable(False)
+        if not torch.equal(out[W:n].view(torch.int32), ref.view(torch.int32)):
+            raise SystemExit("bench: eager and graph outputs differ")
+        us_step = elapsed / steps * 1e6
+        bytes_step = float(touched[W:n].mean())
+        gbps = bytes_step / us_step / 1e3
+        tflops = sh.flops(T) / us_step / 1e6
+        avg = {k: round(v[1] / v[0], 3) for k, v in stats.items()}
+        label = f"{name} T={T}" + ("" if name == "C1" else (" Zipf" if zipf else " uniform"))
+        line = {
+            "metric": f"MoE-layer us/step at T={T} + achieved HBM GB/s (% of peak) on touched experts",
+            "value": round(us_step, 3), "unit": "us/step", "n_gpus": 1, "steps": steps, "warmup": W,
+            "higher_is_better": False, "dtype": "mxfp4 x q8_0, f32 accumulate", "data": "synthetic",
+            "config": {"workload": label, "hidden": sh.hidden, "ffn": sh.ffn, "experts": sh.n_expert,
+                       "top_k": sh.n_used, "shared": sh.has_shared, "tokens_per_step": T,
+                       "resident_layers_cycled": NL, "timed_as": "hipGraph"},
+            "tokens_per_s": round(T * 1e6 / us_step, 1),
+            "us_per_token": round(us_step / T, 3),
+            "distinct_experts_mean": round(float(distinct[W:n].mean()), 2),
+            "hottest_expert_tokens_mean": round(float(hot[W:n].mean()), 1),
+            "algorithmic_bytes_per_step": round(bytes_step),
+            "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "useful_tflops": round(tflops, 2),
+            "mfma_frac_of_fp4_peak": round(tflops / MFMA_FP4_PEAK_TFLOPS, 5),
+            "kernel_avg_us": avg,
+        }
+        log(f"{label}: {us_step:.1f} us/step, {gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS:.1%}), "
+            f"{distinct[W:n].mean():.1f} distinct experts, kernels {avg}")
+        print(json.dumps(line), flush=True)
+        gk.close()
+        if gw is not None:
+            gw.close()
+        del x, logits, ids, wts, out, ref
+    blk.close()
+
 
 def main():
     args = parse()
@@ -133,6 +314,10 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the multi-GPU "
               f"sharding of the block is design-only", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload != "c2":
+        bench_config(args)
+        return
 
     import numpy as np
     import torch

@@ -12,80 +12,150 @@
 #pragma once
 
 #include "device_common.h"
+#include "kernels_rows.h"  // stage_quant
 
 #define MOE_GROUP_MAX_E 1024
-#define MOE_GROUP_MAX_PAIRS 16384
+#define MOE_GROUP_MAX_PAIRS 65535  // grouped rows are kept in 16 bits in k_group
+#define MOE_GROUP_QBLOCKS 512  // x blocks quantized per extra workgroup of k_group
 
-// Workspace words for the grouped chain: counts[E] offsets[E+1] perm[P]
-// inv[P] act[E+2] (act[0] = number of active experts, act[1..] their ids in
-// ascending order).
-static inline size_t group_ws_words(int T, int k, int E) {
-  const size_t P = (size_t)T * k;
-  return (size_t)E + (E + 1) + 2 * P + (E + 2);
+// Item capacity of a call with T tokens, top-k, E experts and items of at
+// most BT rows: ceil(c_e / BT) per expert sums to at most P/BT + min(P, E),
+// plus ceil(T / BT) items of the shared expert.
+static inline int group_item_cap(int T, int k, int E, int BT) {
+  const int P = T * k;
+  return (P + BT - 1) / BT + (P < E ? P : E) + (T + BT - 1) / BT;
 }
 
-__global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids, int P, int E,
-                                                int32_t *__restrict__ counts,
+// Workspace words for the grouped chain: counts[E] offsets[E+1] perm[P]
+// inv[P], then the item list (4-word header, 4 words per item) sized for
+// BT = 1.
+static inline size_t group_ws_words(int T, int k, int E) {
+  const size_t P = (size_t)T * k;
+  return (size_t)E + (E + 1) + 2 * P + 4 + 4 * (size_t)group_item_cap(T, k, E, 1);
+}
+
+// Lanes of the wave holding the same expert id as this lane (e >= 0, ids
+// below 2^10), from one ballot per id bit.
+__device__ __forceinline__ uint64_t same_id_lanes(int e, bool valid) {
+  uint64_t m = __ballot(valid);
+#pragma unroll
+  for (int b = 0; b < 10; b++) {
+    const uint64_t B = __ballot(valid && ((e >> b) & 1));
+    m &= ((e >> b) & 1) ? B : ~B;
+  }
+  return m;
+}
+
+// Workgroup 0: the grouping.  Wave w owns the pairs [w*PW, (w+1)*PW) and
+// walks them 64 at a time in pair order; lanes with the same expert are
+// found by ballots over the id bits (rank = same-expert lanes below).
+//   pass 1: per-wave counts wc[w][e] (one writer per expert per step);
+//   then the histogram (sum over waves), exclusive scans over experts of
+//   the counts and of the item counts ceil(c_e / BT), the item list
+//   (items != NULL: {expert, first row, rows, 0} per item in expert order,
+//   then the shared expert's {E, P + j*BT, rows, 1} when `shared`), and
+//   wc[w][e] turned into wave w's first row of expert e;
+//   pass 2: row of a pair = wc[w][e] + rank, so rows ascend in pair order
+//   within each expert (ggml mul_mat_id's order).
+// Workgroups 1..: Q8_0 of x (T rows of H, flat n_xblocks blocks) into the
+// staged format of the grouped kernels (xq, xd), MOE_GROUP_QBLOCKS blocks
+// each; none when xq is NULL.
+__global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids, int P, int E, int T, int shared,
+                                                int BT, int32_t *__restrict__ counts,
                                                 int32_t *__restrict__ offsets,
                                                 int32_t *__restrict__ perm, int32_t *__restrict__ inv,
-                                                int32_t *__restrict__ act) {
-  __shared__ int32_t sid[MOE_GROUP_MAX_PAIRS];
-  __shared__ int32_t cnt[MOE_GROUP_MAX_E];
-  __shared__ int32_t wsum[16], wflag[16];
+                                                int32_t *__restrict__ items, const float *__restrict__ x,
+                                                int n_xblocks, uint32_t *__restrict__ xq, float *__restrict__ xd) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  for (int e = tid; e < E; e += 1024) cnt[e] = 0;
+  if (blockIdx.x > 0) {
+    const int b0 = (blockIdx.x - 1) * MOE_GROUP_QBLOCKS;
+    const int nb = n_xblocks - b0 < MOE_GROUP_QBLOCKS ? n_xblocks - b0 : MOE_GROUP_QBLOCKS;
+    if (nb > 0) stage_quant(x + (size_t)b0 * MOE_QK, nb, xq + (size_t)b0 * MOE_XSW, xd + b0, tid, 1024);
+    return;
+  }
+  __shared__ uint16_t wc[16][MOE_GROUP_MAX_E];  // per-wave counts, then per-wave first rows (< 2^16)
+  __shared__ int32_t wsum[16], wsumi[16], tot[1];
+  const int PW = ((P + 15) / 16 + 63) & ~63;    // pairs per wave, whole steps of 64
+  const int p_lo = wave * PW, p_hi = p_lo + PW < P ? p_lo + PW : P;
+  for (int i = tid; i < 16 * MOE_GROUP_MAX_E; i += 1024) (&wc[0][0])[i] = 0;
   __syncthreads();
-  for (int p = tid; p < P; p += 1024) {
-    const int e = ids[p];
-    // out-of-range ids are dropped (the host validates the ids it owns)
-    const bool ok = e >= 0 && e < E;
-    sid[p] = ok ? e : -1;
-    if (ok) atomicAdd(&cnt[e], 1);
-    else if (inv) inv[p] = -1;  // dropped pair: no grouped row
+  for (int pb = p_lo; pb < p_hi; pb += 64) {
+    const int p = pb + lane;
+    const int e = p < p_hi ? ids[p] : -1;
+    const bool ok = e >= 0 && e < E;  // out-of-range ids are dropped (the host validates the ids it owns)
+    const uint64_t m = same_id_lanes(e, ok);
+    const uint64_t below = (1ull << lane) - 1ull, upto = (2ull << lane) - 1ull;
+    if (ok && !(m & ~upto)) wc[wave][e] += (uint16_t)__popcll(m & below) + 1;  // last lane of its expert
   }
   __syncthreads();
-  // exclusive scans over experts of the counts and of the "active" flags
-  const int c = tid < E ? cnt[tid] : 0;
-  const int f = c > 0 ? 1 : 0;
-  int v = c, vf = f;
+  // histogram and exclusive scans over experts of the counts and the item counts
+  int c = 0;
+  if (tid < E)
+    for (int w = 0; w < 16; w++) c += wc[w][tid];
+  const int ni = items ? (c + BT - 1) / BT : 0;
+  int v = c, vi = ni;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int u = __shfl_up(v, off), uf = __shfl_up(vf, off);
+    const int u = __shfl_up(v, off), ui = __shfl_up(vi, off);
     if (lane >= off) {
       v += u;
-      vf += uf;
+      vi += ui;
     }
   }
   if (lane == 63) {
     wsum[wave] = v;
-    wflag[wave] = vf;
+    wsumi[wave] = vi;
   }
   __syncthreads();
-  int base = 0, basef = 0;
+  int base = 0, basei = 0;
   for (int w = 0; w < wave; w++) {
     base += wsum[w];
-    basef += wflag[w];
+    basei += wsumi[w];
   }
-  const int excl = base + v - c, exclf = basef + vf - f;
+  const int excl = base + v - c, excli = basei + vi - ni;
   if (tid < E) {
     counts[tid] = c;
     offsets[tid] = excl;
-    if (f && act) act[1 + exclf] = tid;
+    int run = excl;
+    for (int w = 0; w < 16; w++) {
+      const int n = wc[w][tid];
+      wc[w][tid] = (uint16_t)run;
+      run += n;
+    }
+    int4 *rec = items ? reinterpret_cast<int4 *>(items) + 1 + excli : nullptr;
+    for (int j = 0; j < ni; j++) {
+      const int r = j * BT;
+      rec[j] = make_int4(tid, excl + r, c - r < BT ? c - r : BT, 0);
+    }
   }
   if (tid == 1023) {  // thread 1023's inclusive sums are the totals
     offsets[E] = base + v;
-    if (act) act[0] = basef + vf;
+    tot[0] = basei + vi;
   }
-  // stable placement: expert e's thread appends its pairs in pair order
-  if (tid < E && c > 0) {
-    int r = excl;
-    for (int p = 0; p < P; p++) {
-      if (sid[p] == tid) {
-        perm[r] = p;
-        if (inv) inv[p] = r;
-        r++;
-      }
+  __syncthreads();
+  if (items) {
+    const int ns = shared ? (T + BT - 1) / BT : 0;
+    for (int j = tid; j < ns; j += 1024) {
+      const int r = j * BT;
+      reinterpret_cast<int4 *>(items)[1 + tot[0] + j] = make_int4(E, P + r, T - r < BT ? T - r : BT, 1);
     }
+    if (tid == 0) items[0] = tot[0] + ns;
+  }
+  for (int pb = p_lo; pb < p_hi; pb += 64) {
+    const int p = pb + lane;
+    const int e = p < p_hi ? ids[p] : -1;
+    const bool ok = e >= 0 && e < E;
+    const uint64_t m = same_id_lanes(e, ok);
+    const uint64_t below = (1ull << lane) - 1ull, upto = (2ull << lane) - 1ull;
+    const int rank = __popcll(m & below);
+    if (ok) {
+      const int pos = wc[wave][e] + rank;
+      perm[pos] = p;
+      if (inv) inv[p] = pos;
+    } else if (p < p_hi && inv) {
+      inv[p] = -1;  // dropped pair: no grouped row
+    }
+    if (ok && !(m & ~upto)) wc[wave][e] += (uint16_t)(rank + 1);
   }
 }
 

@@ -663,88 +663,11 @@ __global__ __launch_bounds__(1024) void k_down_dec(
   }
 }
 
-// Grouped down (T > 1, x router weight): one workgroup of 4 waves per
-// (32-row unit of H, expert), the waves splitting F; partials meet in LDS.
-// y[hrow][H] = (down_row . h[hrow]) * w   (w = wts[pair] for routed rows).
-// grid (H/32, ny), 256 threads.
-template <int NP>
-__global__ __launch_bounds__(64 * MOE_GRP_WAVES) void k_down_grp(
-    const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
-    const int32_t *__restrict__ offsets, const int32_t *__restrict__ perm,
-    const int32_t *__restrict__ act, const float *__restrict__ wts, int k, int E, int shared, int T, int F, int H,
-    float *__restrict__ y) {
-  extern __shared__ __align__(16) uint32_t lds[];
-  constexpr int NTOK = 2 * NP;
-  const int NQ = F / 128, NQ4 = moe_nq4(NQ), U = F / MOE_UNIT, tiles = H / MOE_TILE;
-  const int NBW = wave_blocks(NQ, MOE_GRP_WAVES);
-  const int wave_words = 4 + NTOK * NBW * (MOE_XSW + 1);
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int P = T * k;
-  const unit_t un = unit_of(blockIdx.y, gridDim.y, true, nullptr, offsets, act, k, E, shared, P, T);
-  if (!un.valid) return;
-  const int u = blockIdx.x;
-  int q0, q1;
-  wave_quads(NQ, MOE_GRP_WAVES, wave, q0, q1);
-  const int nb = 4 * (q1 - q0);
-  uint32_t *xs = lds + (size_t)wave * wave_words;
-  float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)NTOK * NBW * MOE_XSW);
-  float *red = reinterpret_cast<float *>(lds);  // [wave][2 tiles][NTOK][16]
-  const size_t t0 = (size_t)un.mat * tiles + 2 * u;
-  const wstream ws[2] = {make_wstream(w_d, t0, NQ4), make_wstream(w_d, t0 + 1, NQ4)};
-  for (int i0 = 0; i0 < un.nrows; i0 += NTOK) {
-    const int nt = un.nrows - i0 < NTOK ? un.nrows - i0 : NTOK;
-    kring<2, 4> ring;
-    kloop_prime<2, 4>(ring, ws, q0, q1, lane);
-    if (lane < 4) xs[lane] = 0u;
-    for (int t = 0; t < nt; t++) {
-      const size_t hrow = (size_t)(un.row0 + i0 + t);
-      stage_copy<false>(hs + (hrow * U + (size_t)4 * q0) * MOE_XSW, hd + hrow * U + (size_t)4 * q0, nb,
-                        xs + 4 + (size_t)t * NBW * MOE_XSW, dy + (size_t)t * NBW, lane);
-    }
-    __syncthreads();
-    bsel bs[NP];
-#pragma unroll
-    for (int p = 0; p < NP; p++)
-      bs[p] = make_bsel(lane, 4 + 2 * p * NBW * MOE_XSW, 4 + (2 * p + 1) * NBW * MOE_XSW, 2 * p * NBW,
-                        (2 * p + 1) * NBW, 2 * p < nt, 2 * p + 1 < nt, 0);
-    f32x4_t acc[NP][2];
-    kloop<2, NP, 4>(ring, ws, q0, q1, bs, xs, dy, lane, acc);
-    __syncthreads();
-    const int gb = lane >> 4, tp = (lane >> 3) & 1;
-#pragma unroll
-    for (int p = 0; p < NP; p++)
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-          const float v = col8_sum(acc[p][i][r]);
-          if ((lane & 7) == 0) red[((wave * 2 + i) * NTOK + 2 * p + tp) * MOE_TILE + 4 * gb + r] = v;
-        }
-    __syncthreads();
-    // thread (token slot t = idx / 32, row j = idx % 32)
-    for (int idx = threadIdx.x; idx < nt * MOE_UNIT; idx += 64 * MOE_GRP_WAVES) {
-      const int t = idx >> 5, j = idx & 31, ti = j >> 4, rr = j & 15;
-      float v = 0.0f;
-      for (int w = 0; w < MOE_GRP_WAVES; w++) v += red[((w * 2 + ti) * NTOK + t) * MOE_TILE + rr];
-      const int hrow = un.row0 + i0 + t;
-      if (!un.shared) v = __fmul_rn(v, wts[perm[hrow]]);
-      y[(size_t)hrow * H + (size_t)u * MOE_UNIT + j] = v;
-    }
-    __syncthreads();
-  }
-}
-
 // LDS bytes of the kernels.
 static inline size_t gate_up_lds_bytes(int H, int NP) {
   const int NBW = wave_blocks(H / 128, MOE_GU_KS);
   const size_t stage = ((size_t)4 + (size_t)2 * NP * NBW * (MOE_XSW + 1)) * 4 * MOE_GU_KS;
   const size_t red = (size_t)4 * 2 * 2 * NP * MOE_TILE * 4;
-  return stage > red ? stage : red;
-}
-static inline size_t grp_lds_bytes(int K, int NP, int streams) {
-  const int NBW = wave_blocks(K / 128, MOE_GRP_WAVES);
-  const size_t stage = ((size_t)4 + (size_t)2 * NP * NBW * (MOE_XSW + 1)) * 4 * MOE_GRP_WAVES;
-  const size_t red = (size_t)MOE_GRP_WAVES * streams * 2 * NP * MOE_TILE * 4;
   return stage > red ? stage : red;
 }
 static inline size_t down_dec_lds_bytes(int F, int S) {

@@ -10,6 +10,7 @@
 #include "device_common.h"
 #include "kernels_decode.h"
 #include "kernels_group.h"
+#include "kernels_grouped.h"
 #include "kernels_rows.h"
 #include "kernels_weights.h"
 
@@ -48,6 +49,7 @@ struct scratch {
   uint32_t *hq = nullptr; float *hd = nullptr;     // staged h: [P+T][F/32][16] dwords, [P+T][F/32]
   float *htap = nullptr;                           // [P+T][F]
   float *y = nullptr;                              // [P+T][H]
+  uint32_t *xq = nullptr; float *xd = nullptr;     // staged x of the grouped chain: [T][H/32][16] dwords, [T][H/32]
   int32_t *grp = nullptr;                          // grouping workspace
   size_t grp_words = 0;
   // split-K decode: chunk partial sums and per-unit tickets (the tickets are
@@ -189,7 +191,7 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 // scratch
 
 static void scratch_free(scratch &s) {
-  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf};
+  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   s = scratch();
@@ -211,6 +213,8 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipMalloc(&s.hd, R * (F / 32) * 4));
   HIPC(c, hipMalloc(&s.htap, R * F * 4));
   HIPC(c, hipMalloc(&s.y, R * H * 4));
+  HIPC(c, hipMalloc(&s.xq, (size_t)T * (H / 32) * 64));
+  HIPC(c, hipMalloc(&s.xd, (size_t)T * (H / 32) * 4));
   s.grp_words = group_ws_words(T, k, E);
   HIPC(c, hipMalloc(&s.grp, s.grp_words * 4));
   HIPC(c, hipMalloc(&s.x_in, (size_t)T * H * 4));
@@ -481,53 +485,22 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
   HIPC(c, hipSetDevice(c->device));
   {
     prof_scope ps(c, K_GROUP, (hipStream_t)stream);
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, counts, offsets,
-                       perm, inv, (int32_t *)nullptr);
+    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, T, 0, 1, counts,
+                       offsets, perm, inv, (int32_t *)nullptr, (const float *)nullptr, 0, (uint32_t *)nullptr,
+                       (float *)nullptr);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
 
-// Token pairs per pass of the workgroup kernels: as many as fit the 64 KiB of
-// LDS a workgroup can address without an attribute.
-static int pick_np(int K, int streams) {
-  if (grp_lds_bytes(K, 4, streams) <= 65536) return 4;
-  if (grp_lds_bytes(K, 2, streams) <= 65536) return 2;
-  return grp_lds_bytes(K, 1, streams) <= 65536 ? 1 : 0;
-}
-static int pick_np_gate_up(int H) {
-  if (gate_up_lds_bytes(H, 4) <= 65536) return 4;
-  if (gate_up_lds_bytes(H, 2) <= 65536) return 2;
-  return gate_up_lds_bytes(H, 1) <= 65536 ? 1 : 0;
-}
-
-// gate/up launch; grouped == 0: decode, columns are slots (ids), one token.
-static void launch_gate_up(int NP, dim3 g, hipStream_t st, const dev_layer &L, const float *x, int grouped,
-                           const int32_t *ids, const int32_t *offsets, const int32_t *perm, const int32_t *act,
-                           int shared, int T, uint32_t *hq, float *hd, float *htap) {
+// decode gate/up launch (k_gate_up with one token, columns = slots)
+static void launch_gate_up_decode(dim3 g, hipStream_t st, const dev_layer &L, const float *x, const int32_t *ids,
+                                  int shared, uint32_t *hq, float *hd, float *htap) {
   const moe_layer_desc &d = L.d;
-  const size_t lds = gate_up_lds_bytes(d.hidden, NP);
-#define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, x, grouped, ids, offsets, perm, act, d.n_used, \
-                    d.n_expert, shared, T, d.ffn, d.hidden, d.clamp, hq, hd, htap
-  const dim3 blk(64 * 2 * MOE_GU_KS);
-  if (NP == 4) hipLaunchKernelGGL(k_gate_up<4>, g, blk, lds, st, MOE_GU_ARGS);
-  else if (NP == 2) hipLaunchKernelGGL(k_gate_up<2>, g, blk, lds, st, MOE_GU_ARGS);
-  else hipLaunchKernelGGL(k_gate_up<1>, g, blk, lds, st, MOE_GU_ARGS);
-#undef MOE_GU_ARGS
-}
-
-static void launch_down_grp(int NP, dim3 g, hipStream_t st, const dev_layer &L, const uint32_t *hq, const float *hd,
-                            const int32_t *offsets, const int32_t *perm, const int32_t *act, const float *wts,
-                            int shared, int T, float *y) {
-  const moe_layer_desc &d = L.d;
-  const size_t lds = grp_lds_bytes(d.ffn, NP, 2);
-#define MOE_DN_ARGS L.m[T_DOWN].w, hq, hd, offsets, perm, act, wts, d.n_used, d.n_expert, shared, T, d.ffn, \
-                    d.hidden, y
-  const dim3 blk(64 * MOE_GRP_WAVES);
-  if (NP == 4) hipLaunchKernelGGL(k_down_grp<4>, g, blk, lds, st, MOE_DN_ARGS);
-  else if (NP == 2) hipLaunchKernelGGL(k_down_grp<2>, g, blk, lds, st, MOE_DN_ARGS);
-  else hipLaunchKernelGGL(k_down_grp<1>, g, blk, lds, st, MOE_DN_ARGS);
-#undef MOE_DN_ARGS
+  hipLaunchKernelGGL(k_gate_up<1>, g, dim3(64 * 2 * MOE_GU_KS), gate_up_lds_bytes(d.hidden, 1), st, L.m[T_GATE].w,
+                     L.m[T_UP].w, x, 0, ids, (const int32_t *)nullptr, (const int32_t *)nullptr,
+                     (const int32_t *)nullptr, d.n_used, d.n_expert, shared, 1, d.ffn, d.hidden, d.clamp, hq, hd,
+                     htap);
 }
 
 static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
@@ -550,7 +523,7 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
     return forward_grouped(c, L, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
   {
     prof_scope pg(c, K_GU_DECODE, st);
-    launch_gate_up(1, dim3(F / MOE_UNIT, S), st, L, x, 0, ids, nullptr, nullptr, nullptr, shared, 1, s.hq, s.hd, htap);
+    launch_gate_up_decode(dim3(F / MOE_UNIT, S), st, L, x, ids, shared, s.hq, s.hd, htap);
   }
   s.h_rows = htap ? (size_t)S : 0;
   s.last_F = F;
@@ -564,40 +537,55 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   return MOE_OK;
 }
 
-// The grouped chain for T > 1.
+// Token pairs of the largest work item of the grouped chain (items hold up
+// to 2 * NPMAX grouped rows of one expert).
+static int pick_npmax(int T) { return T <= 4 ? 2 : 4; }
+
+// The grouped chain for T > 1, four launches: k_group (grouping, work items,
+// and Q8_0 of x by its extra workgroups) -> gate/up per (32-row unit, item)
+// -> down per (128 rows of H, item) -> combine in slot order.
 static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
                                   int T, float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
-  const int k = d.n_used, E = d.n_expert, P = T * k;
+  const int k = d.n_used, E = d.n_expert, P = T * k, H = d.hidden, F = d.ffn;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
   const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
-  const int np_gu = pick_np_gate_up(d.hidden), np_dn = pick_np(d.ffn, 2);
-  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E || !np_gu || !np_dn)
-    return fail(c, MOE_ERR_UNSUPPORTED, "grouped: shape outside kernel range");
+  if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E)
+    return fail(c, MOE_ERR_UNSUPPORTED, "grouped: more than %d pairs or %d experts", MOE_GROUP_MAX_PAIRS,
+                MOE_GROUP_MAX_E);
+  const int NPM = pick_npmax(T), BT = 2 * NPM;
   scratch &s = c->sc;
-  int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *act = inv + P;
+  int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
   float *htap = c->taps ? s.htap : nullptr;
+  const int n_xblocks = T * (H / MOE_QK);
   {
     prof_scope pgr(c, K_GROUP, st);
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, st, ids, P, E, counts, offsets, perm, inv, act);
+    hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
+                       shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd);
   }
-  const int ny = (P < E ? P : E) + shared;
+  const int cap = group_item_cap(T, k, E, BT);
   {
     prof_scope pg(c, K_GU_GROUPED, st);
-    launch_gate_up(np_gu, dim3(d.ffn / MOE_UNIT, ny), st, L, x, 1, ids, offsets, perm, act, shared, T, s.hq, s.hd,
-                   htap);
+#define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
+    const dim3 g(F / MOE_UNIT, cap), b(256);
+    if (NPM == 4) hipLaunchKernelGGL(k_gate_up_g<4>, g, b, 0, st, MOE_GU_ARGS);
+    else hipLaunchKernelGGL(k_gate_up_g<2>, g, b, 0, st, MOE_GU_ARGS);
+#undef MOE_GU_ARGS
   }
   s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
-  s.last_F = d.ffn;
+  s.last_F = F;
   {
     prof_scope pd(c, K_DOWN_GROUPED, st);
-    launch_down_grp(np_dn, dim3(d.hidden / MOE_UNIT, ny), st, L, s.hq, s.hd, offsets, perm, act, wts, shared, T,
-                    s.y);
+#define MOE_DN_ARGS L.m[T_DOWN].w, s.hq, s.hd, P + T, items, perm, wts, F, H, s.y
+    const dim3 g(ceil_div(H / (2 * MOE_TILE), MOE_DG_WAVES), cap), b(64 * MOE_DG_WAVES);
+    if (NPM == 4) hipLaunchKernelGGL(k_down_g<4>, g, b, 0, st, MOE_DN_ARGS);
+    else hipLaunchKernelGGL(k_down_g<2>, g, b, 0, st, MOE_DN_ARGS);
+#undef MOE_DN_ARGS
   }
   {
     prof_scope pc(c, K_COMBINE, st);
-    hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * d.hidden, 256)), dim3(256), 0, st, s.y, inv, T, k,
-                       d.hidden, shared, per_slot ? 1 : 0, out);
+    hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * H, 256)), dim3(256), 0, st, s.y, inv, T, k, H, shared,
+                       per_slot ? 1 : 0, out);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;

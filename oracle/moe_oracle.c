@@ -262,6 +262,7 @@ typedef struct {
   int8_t *xq;     /* [T][H]   */
   uint16_t *xd;   /* [T][H/32] */
   float *h;       /* [P+T][F] routed pairs then shared rows */
+  const float *h_in; /* if set: h is given (same layout), gate/up/SwiGLU skipped */
   int8_t *hq;     /* [P+T][F] */
   uint16_t *hd;   /* [P+T][F/32] */
   float *y;       /* [P+T][H] weighted routed rows, then shared rows */
@@ -297,7 +298,8 @@ static void *fwd_worker(void *argp) {
 
   /* gate / up / clamp / SwiGLU for every (expert row, ffn column) */
   span((size_t)R * F, a->tid, S->nthreads, &b, &e);
-  for (size_t i = b; i < e; i++) {
+  for (size_t i = b; i < e && S->h_in; i++) S->h[i] = S->h_in[i];
+  for (size_t i = b; i < e && !S->h_in; i++) {
     const int r = (int)(i / (size_t)F), c = (int)(i % (size_t)F);
     const uint8_t *gw, *uw;
     int t;
@@ -357,11 +359,27 @@ static void *fwd_worker(void *argp) {
   return NULL;
 }
 
+static int forward_impl(const mo_layer *L, int T, const float *x, const int32_t *ids, const float *wts,
+                        const float *h_in, float *out, float *per_slot, float *h_routed, float *h_shared,
+                        int n_threads);
+
 int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
                         const int32_t *ids, const float *wts, float *out,
                         float *per_slot, float *h_routed, float *h_shared,
                         int n_threads) {
-  if (!L || T <= 0 || !x || !ids || !wts || !out) return -1;
+  return forward_impl(L, T, x, ids, wts, NULL, out, per_slot, h_routed, h_shared, n_threads);
+}
+
+int mo_moe_forward_from_h(const mo_layer *L, int T, const int32_t *ids, const float *wts,
+                          const float *h, float *out, float *per_slot, int n_threads) {
+  if (!h) return -1;
+  return forward_impl(L, T, NULL, ids, wts, h, out, per_slot, NULL, NULL, n_threads);
+}
+
+static int forward_impl(const mo_layer *L, int T, const float *x, const int32_t *ids, const float *wts,
+                        const float *h_in, float *out, float *per_slot, float *h_routed, float *h_shared,
+                        int n_threads) {
+  if (!L || T <= 0 || (!x && !h_in) || !ids || !wts || !out) return -1;
   if (L->H % MO_QK || L->F % MO_QK || L->k <= 0 || L->E <= 0) return -1;
   for (int p = 0; p < T * L->k; p++) {
     if (ids[p] < 0 || ids[p] >= L->E || !L->gate[ids[p]] || !L->up[ids[p]] ||
@@ -379,6 +397,7 @@ int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
   S.P = P;
   S.nthreads = n_threads;
   S.x = x;
+  S.h_in = h_in;
   S.ids = ids;
   S.wts = wts;
   S.out = out;
@@ -393,7 +412,7 @@ int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
     return -1;
   }
   /* src1 -> Q8_0, once per token (mul_mat_id broadcasts x over slots) */
-  for (int t = 0; t < T; t++) {
+  for (int t = 0; t < T && x; t++) {
     mo_quantize_q8_0(x + (size_t)t * H, H, S.xq + (size_t)t * H,
                      S.xd + (size_t)t * (H / MO_QK));
   }

@@ -121,6 +121,13 @@ int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
                         float *per_slot, float *h_routed, float *h_shared,
                         int n_threads);
 
+/* The same block from a given h [P+T][F] (routed pairs t*k+s, then the
+ * shared expert's T rows): Q8_0 of h, down, router weight, combine.  Lets a
+ * test reproduce the activation quantization of another implementation's
+ * h exactly. */
+int mo_moe_forward_from_h(const mo_layer *L, int T, const int32_t *ids, const float *wts,
+                          const float *h, float *out, float *per_slot, int n_threads);
+
 /* ---- synthetic weights ------------------------------------------------ */
 
 /* SplitMix64 finalizer (Steele, Lea, Flood 2014). */

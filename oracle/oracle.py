@@ -77,6 +77,9 @@ def lib():
         L.mo_moe_forward_taps.restype = ctypes.c_int
         L.mo_moe_forward_taps.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _f32p, _i32p, _f32p, _f32p,
                                           _f32p, _f32p, _f32p, ctypes.c_int]
+        L.mo_moe_forward_from_h.restype = ctypes.c_int
+        L.mo_moe_forward_from_h.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _i32p, _f32p, _f32p, _f32p,
+                                            _f32p, ctypes.c_int]
         L.mo_mix64.restype = ctypes.c_uint64
         L.mo_mix64.argtypes = [ctypes.c_uint64]
         L.mo_gen_key.restype = ctypes.c_uint64
@@ -255,3 +258,25 @@ class OracleLayer:
             res["h"] = hr
             res["h_shared"] = hs
         return res
+
+    def forward_from_h(self, ids: np.ndarray, wts: np.ndarray, h: np.ndarray, h_shared=None,
+                       n_threads: int = 1) -> np.ndarray:
+        """The block from a given SwiGLU output: h f32 [T, k, F] (and the
+        shared expert's [T, F]) -> Q8_0(h) -> down x router weight ->
+        combine -> out f32 [T, H].  A test passes another implementation's
+        h here to reproduce its activation quantization exactly."""
+        ids = np.ascontiguousarray(ids, np.int32)
+        wts = np.ascontiguousarray(wts, np.float32)
+        T = ids.shape[0]
+        rows = [np.asarray(h, np.float32).reshape(T * self.k, self.F)]
+        if self.shared:
+            rows.append(np.asarray(h_shared, np.float32).reshape(T, self.F))
+        hh = np.ascontiguousarray(np.concatenate(rows, axis=0), np.float32)
+        out = np.empty((T, self.H), np.float32)
+        s, keep = self._struct()
+        rc = lib().mo_moe_forward_from_h(ctypes.byref(s), T, _p(ids, _i32p), _p(wts, _f32p), _p(hh, _f32p),
+                                         _p(out, _f32p), None, int(n_threads))
+        del keep
+        if rc != 0:
+            raise ValueError("oracle forward_from_h rejected its arguments")
+        return out

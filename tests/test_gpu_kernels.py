@@ -140,3 +140,34 @@ def test_group_bit_exact(blk, torch_dev, oracle, T, k, E, zipf):
     g = oracle.group(ids_np, E)
     for name, t in (("counts", counts), ("offsets", offsets), ("perm", perm), ("inv", inv)):
         np.testing.assert_array_equal(t.cpu().numpy(), g[name], err_msg=name)
+
+
+@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32)])
+def test_group_drops_out_of_range_ids(blk, torch_dev, T, k, E):
+    """Out-of-range ids get no grouped row (inv = -1); the valid pairs keep
+    ascending pair order within each expert (checked against a stable sort)."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(T + E)
+    ids_np = rng.integers(0, E, size=(T, k), dtype=np.int32)
+    bad = rng.random((T, k)) < 0.1
+    ids_np[bad] = np.where(rng.random(int(bad.sum())) < 0.5, -1, E).astype(np.int32)
+    say("group with dropped ids", T, k, E, int(bad.sum()))
+    flat = ids_np.ravel()
+    ok = (flat >= 0) & (flat < E)
+    counts_ref = np.bincount(flat[ok], minlength=E).astype(np.int32)
+    offsets_ref = np.concatenate([[0], np.cumsum(counts_ref)]).astype(np.int32)
+    valid_pairs = np.nonzero(ok)[0]
+    perm_ref = valid_pairs[np.argsort(flat[ok], kind="stable")].astype(np.int32)
+    inv_ref = np.full(T * k, -1, np.int32)
+    inv_ref[perm_ref] = np.arange(len(perm_ref), dtype=np.int32)
+    ids = torch.from_numpy(ids_np).to(dev)
+    counts = torch.empty(E, dtype=torch.int32, device=dev)
+    offsets = torch.empty(E + 1, dtype=torch.int32, device=dev)
+    perm = torch.full((T * k,), -7, dtype=torch.int32, device=dev)
+    inv = torch.empty(T * k, dtype=torch.int32, device=dev)
+    blk.group(ids, E, counts, offsets, perm, inv)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(counts.cpu().numpy(), counts_ref)
+    np.testing.assert_array_equal(offsets.cpu().numpy(), offsets_ref)
+    np.testing.assert_array_equal(perm.cpu().numpy()[: len(perm_ref)], perm_ref)
+    np.testing.assert_array_equal(inv.cpu().numpy(), inv_ref)

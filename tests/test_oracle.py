@@ -278,3 +278,18 @@ def test_generator_distribution(oracle):
     # different (layer, tensor, expert) keys give different bytes
     assert not np.array_equal(b, oracle.gen_mxfp4(99, 0, 0, 6, 512, 2048))
     assert not np.array_equal(b, oracle.gen_mxfp4(99, 0, 1, 5, 512, 2048))
+
+
+def test_forward_from_h_reproduces_forward(oracle):
+    """The oracle's down path from a given h, fed the oracle's own h, is the
+    oracle's forward bit for bit (with and without the shared expert)."""
+    for shared in (False, True):
+        H, F, E, k, T = 256, 128, 8, 2, 3
+        rng = np.random.default_rng(5)
+        x = rng.standard_normal((T, H), dtype=np.float32)
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+        wts = rng.random((T, k), dtype=np.float32)
+        L = oracle.OracleLayer.generated(9, 0, H, F, E, k, experts=list(range(E)), shared=shared)
+        ref = L.forward(x, ids, wts, taps=True)
+        got = L.forward_from_h(ids, wts, ref["h"], ref["h_shared"])
+        np.testing.assert_array_equal(got, ref["out"])
