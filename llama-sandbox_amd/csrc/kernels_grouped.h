@@ -363,3 +363,359 @@ void k_down_g(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, 
   else if (NPMAX >= 2 && nt > 2) dn_item<(NPMAX >= 2 ? 2 : 1)>(w_d, src, it, perm, wts, F, H, y);
   else dn_item<1>(w_d, src, it, perm, wts, F, H, y);
 }
+
+// ===========================================================================
+// Token octets on v_mfma_scale_f32_32x32x64_f8f6f4 (items of up to 8 rows).
+//
+// Lane layout (probed on the device): A lane r + 32*ga holds row r of a
+// 32-row tile and one whole MXFP4 block (its 16 ggml nibble bytes, nibble e
+// at K offset e of the block) with that block's E8M0 exponent as its scale;
+// ga picks the first or second block of the step's block pair.  B lane
+// n + 32*gb holds column n: bytes 0-15 are K offsets 16*gb + [0, 16) of the
+// first block, bytes 16-31 the same offsets of the second block.  D lane
+// n + 32*gb holds column n, rows 8*i + 4*gb + j at element 4*i + j.
+// Block-diagonal B: column n = 4*t + 2*part + g carries part (hi / lo
+// digits) of block g of the pair for token t of the octet, so one MFMA
+// multiplies 32 rows x 2 blocks against 8 tokens, and the 4 columns of a
+// token are added at the end (lanes 4t .. 4t+3).
+//
+// The A operand comes from the 16-row record layout unchanged: rows r < 16
+// of the 32-row tile from tile 2T, r >= 16 from tile 2T+1 (the next
+// record run); block 2j + ga of quad q is lane (r % 16) + 16*(2j + ga) of
+// that tile's quad, and its exponent byte q % 4 of the same lane's exponent
+// dword.
+
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
+
+// A 32-row tile: 16-row tiles tile16 and tile16 + 1 of the tensor.
+__device__ __forceinline__ wstream make_wstream32(const uint8_t *w, size_t tile16, int NG) {
+  wstream s;
+  s.rec = __builtin_amdgcn_make_buffer_rsrc((void *)(w + tile16 * NG * MOE_REC_BYTES), 0, 2 * NG * MOE_REC_BYTES,
+                                            MOE_RSRC_FLAGS);
+  return s;
+}
+
+// This lane's A byte offsets (step 0 of a quad): data, exponent dword.
+struct aoff32 {
+  uint32_t v, s;
+};
+
+__device__ __forceinline__ aoff32 make_aoff32(int lane, int NG) {
+  const int r = lane & 31, ga = lane >> 5;
+  const uint32_t tb = (uint32_t)(r >> 4) * NG * MOE_REC_BYTES;
+  const uint32_t l16 = (uint32_t)((r & 15) + 16 * ga);
+  aoff32 a;
+  a.v = tb + l16 * 16;
+  a.s = tb + MOE_REC_SC + l16 * 4;
+  return a;
+}
+
+template <int NW>
+struct wq32 {
+  u32x4_t w[NW][2];  // [stream][step]
+};
+
+template <int NW, int CPOL>
+__device__ __forceinline__ void load_wq32(wq32<NW> &b, const wstream (&ws)[NW], const aoff32 &ao, int q) {
+#pragma unroll
+  for (int i = 0; i < NW; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      b.w[i][j] = __builtin_amdgcn_raw_buffer_load_b128(ws[i].rec, ao.v + j * 512,
+                                                        (q >> 2) * MOE_REC_BYTES + (q & 3) * 1024, CPOL);
+}
+
+template <int NW>
+__device__ __forceinline__ void load_sc32(uint32_t (&sc)[NW][2], const wstream (&ws)[NW], const aoff32 &ao, int g4) {
+#pragma unroll
+  for (int i = 0; i < NW; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+      sc[i][j] = __builtin_amdgcn_raw_buffer_load_b32(ws[i].rec, ao.s + j * 128, g4 * MOE_REC_BYTES, 0);
+}
+
+// B source of this lane for one octet: row = the staged row of token
+// t = n / 4 of the octet (< 0: absent).
+__device__ __forceinline__ gsel make_gsel32(int lane, int row, int KB) {
+  const int n = lane & 31, gb = lane >> 5;
+  const int part = (n >> 1) & 1, g = n & 1;
+  gsel s;
+  s.voff = row >= 0 ? (uint32_t)((row * KB + g) * (MOE_XSW * 4) + part * 32 + gb * 16) : MOE_OOB;
+  s.doff = row >= 0 ? (uint32_t)((row * KB + g) * 4) : MOE_OOB;
+  return s;
+}
+
+template <int NO>
+struct bq32 {
+  u32x4_t v[NO][2];
+  float d[NO][2];
+};
+
+template <int NO>
+__device__ __forceinline__ void load_bq32(bq32<NO> &b, const gsrc &src, const gsel (&gs)[NO], int q) {
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      b.v[o][j] = __builtin_amdgcn_raw_buffer_load_b128(src.x, gs[o].voff, (4 * q + 2 * j) * MOE_XSW * 4, 0);
+      b.d[o][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, gs[o].doff,
+                                                                                 (4 * q + 2 * j) * 4, 0));
+    }
+}
+
+template <int SEL, int NW, int NO>
+__device__ __forceinline__ void quad_mma32(const wq32<NW> &w, const uint32_t (&sc)[NW][2], const bq32<NO> &b,
+                                           bool upper, int sb, f32x16_t (&acc)[NO][NW]) {
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+      const u32x4_t v = b.v[o][j];
+      i32x8_t bv;
+      bv[0] = upper ? 0 : (int)v.x; bv[1] = upper ? 0 : (int)v.y; bv[2] = upper ? 0 : (int)v.z; bv[3] = upper ? 0 : (int)v.w;
+      bv[4] = upper ? (int)v.x : 0; bv[5] = upper ? (int)v.y : 0; bv[6] = upper ? (int)v.z : 0; bv[7] = upper ? (int)v.w : 0;
+#pragma unroll
+      for (int i = 0; i < NW; i++) {
+        const u32x4_t a4 = w.w[i][j];
+        const i32x8_t a = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
+        f32x16_t z;
+#pragma unroll
+        for (int e = 0; e < 16; e++) z[e] = 0.0f;
+        const f32x16_t r = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bv, z, 4, 0, SEL, (int)sc[i][j], 0, sb);
+        acc[o][i] = acc[o][i] + b.d[o][j] * r;
+      }
+    }
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int i = 0; i < NW; i++) asm volatile("" : "+v"(acc[o][i]));
+}
+
+__device__ __forceinline__ bool lane_upper32(int lane) { return (lane & 1) != 0; }      // second block of the pair
+__device__ __forceinline__ int lane_bscale32(int lane) { return (lane & 2) ? 127 : 131; }  // lo : hi digits
+
+// Ring state of an octet K loop: weights of 4 quads, B data of 4 quads,
+// exponent dwords of NG groups.  Every index into it is a template
+// constant (the steps below are instantiated per quad), so the arrays stay
+// in registers.
+template <int NW, int NO, int NG>
+struct oring {
+  wq32<NW> w[4];
+  bq32<NO> b[4];
+  uint32_t sc[NG][NW][2];
+};
+
+// One quad of the loop: issue B for quad qB into slot SLOT+2 and weights
+// for quad qW into slot SLOT+3 (if wanted), then multiply slot SLOT with
+// exponent group G (op_sel SEL = quad % 4).
+template <int SEL, int SLOT, int G, bool WB, bool WW, int NW, int NO, int NG, int CPOL>
+__device__ __forceinline__ void ostep(oring<NW, NO, NG> &r, const wstream (&ws)[NW], const aoff32 &ao,
+                                      const gsrc &src, const gsel (&gs)[NO], int qB, int qW, bool upper, int sb,
+                                      f32x16_t (&acc)[NO][NW]) {
+  if constexpr (WB) load_bq32<NO>(r.b[(SLOT + 2) & 3], src, gs, qB);
+  if constexpr (WW) load_wq32<NW, CPOL>(r.w[(SLOT + 3) & 3], ws, ao, qW);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  quad_mma32<SEL, NW, NO>(r.w[SLOT], r.sc[G], r.b[SLOT], upper, sb, acc);
+}
+
+// Quads QL .. NQW-1 of a fully unrolled loop from q0 (q0 % 4 == 0).
+template <int QL, int NQW, int NW, int NO, int NG, int CPOL>
+__device__ __forceinline__ void ofixed_from(oring<NW, NO, NG> &r, const wstream (&ws)[NW], const aoff32 &ao,
+                                            int q0, const gsrc &src, const gsel (&gs)[NO], bool upper, int sb,
+                                            f32x16_t (&acc)[NO][NW]) {
+  if constexpr (QL < NQW) {
+    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<NW>(r.sc[(QL >> 2) + 1], ws, ao, (q0 >> 2) + (QL >> 2) + 1);
+    ostep<QL & 3, QL & 3, QL / 4, (QL + 2 < NQW), (QL + 3 < NQW), NW, NO, NG, CPOL>(
+        r, ws, ao, src, gs, q0 + QL + 2, q0 + QL + 3, upper, sb, acc);
+    ofixed_from<QL + 1, NQW, NW, NO, NG, CPOL>(r, ws, ao, q0, src, gs, upper, sb, acc);
+  }
+}
+
+// K loop over NQW quads from q0 (q0 % 4 == 0), fully unrolled; the rings
+// as in gloop_fixed (B 2 quads ahead, weights 3 quads ahead).
+template <int NW, int NO, int CPOL, int NQW>
+__device__ __forceinline__ void oloop_fixed(const wstream (&ws)[NW], const aoff32 &ao, int q0, const gsrc &src,
+                                            const gsel (&gs)[NO], int lane, f32x16_t (&acc)[NO][NW]) {
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[o][i][e] = 0.0f;
+  constexpr int NG = (NQW + 3) / 4;
+  const bool upper = lane_upper32(lane);
+  const int sb = lane_bscale32(lane);
+  oring<NW, NO, NG> r;
+  load_sc32<NW>(r.sc[0], ws, ao, q0 >> 2);
+  load_bq32<NO>(r.b[0], src, gs, q0);
+  load_wq32<NW, CPOL>(r.w[0], ws, ao, q0);
+  if constexpr (NQW > 1) {
+    load_bq32<NO>(r.b[1], src, gs, q0 + 1);
+    load_wq32<NW, CPOL>(r.w[1], ws, ao, q0 + 1);
+  }
+  if constexpr (NQW > 2) load_wq32<NW, CPOL>(r.w[2], ws, ao, q0 + 2);
+  ofixed_from<0, NQW, NW, NO, NG, CPOL>(r, ws, ao, q0, src, gs, upper, sb, acc);
+}
+
+// Run-time number of quads [q0, q1): windows of 4 quads, loads past the
+// end re-read the last quad, guarded tail.
+template <int NW, int NO, int CPOL>
+__device__ __forceinline__ void oloop_rolled(const wstream (&ws)[NW], const aoff32 &ao, int q0, int q1,
+                                             const gsrc &src, const gsel (&gs)[NO], int lane,
+                                             f32x16_t (&acc)[NO][NW]) {
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[o][i][e] = 0.0f;
+  if (q1 <= q0) return;
+  const bool upper = lane_upper32(lane);
+  const int sb = lane_bscale32(lane);
+  const int last = q1 - 1, glast = last >> 2;
+  oring<NW, NO, 1> r;
+  uint32_t scn[NW][2];
+  load_sc32<NW>(r.sc[0], ws, ao, q0 >> 2);
+  load_bq32<NO>(r.b[0], src, gs, q0);
+  load_wq32<NW, CPOL>(r.w[0], ws, ao, q0);
+  load_bq32<NO>(r.b[1], src, gs, q0 + 1 < q1 ? q0 + 1 : last);
+  load_wq32<NW, CPOL>(r.w[1], ws, ao, q0 + 1 < q1 ? q0 + 1 : last);
+  load_wq32<NW, CPOL>(r.w[2], ws, ao, q0 + 2 < q1 ? q0 + 2 : last);
+  auto qc = [&](int q) { return q < q1 ? q : last; };
+  int qb = q0;
+  for (; qb + 4 <= q1; qb += 4) {
+    const int gn = (qb >> 2) + 1;
+    load_sc32<NW>(scn, ws, ao, gn < glast ? gn : glast);
+    ostep<0, 0, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 2), qc(qb + 3), upper, sb, acc);
+    ostep<1, 1, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 3), qc(qb + 4), upper, sb, acc);
+    ostep<2, 2, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 4), qc(qb + 5), upper, sb, acc);
+    ostep<3, 3, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 5), qc(qb + 6), upper, sb, acc);
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+#pragma unroll
+      for (int j = 0; j < 2; j++) r.sc[0][i][j] = scn[i][j];
+  }
+  if (qb < q1) ostep<0, 0, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 2), qc(qb + 3), upper, sb, acc);
+  if (qb + 1 < q1) ostep<1, 1, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 3), qc(qb + 4), upper, sb, acc);
+  if (qb + 2 < q1) ostep<2, 2, 0, true, true, NW, NO, 1, CPOL>(r, ws, ao, src, gs, qc(qb + 4), qc(qb + 5), upper, sb, acc);
+}
+
+template <int NW, int NO, int CPOL>
+__device__ __forceinline__ void oloop_any(const wstream (&ws)[NW], const aoff32 &ao, int q0, int q1,
+                                          const gsrc &src, const gsel (&gs)[NO], int lane,
+                                          f32x16_t (&acc)[NO][NW]) {
+  switch (q1 - q0) {
+    case 28: oloop_fixed<NW, NO, CPOL, 28>(ws, ao, q0, src, gs, lane, acc); break;
+    case 16: oloop_fixed<NW, NO, CPOL, 16>(ws, ao, q0, src, gs, lane, acc); break;
+    case 8: oloop_fixed<NW, NO, CPOL, 8>(ws, ao, q0, src, gs, lane, acc); break;
+    case 6: oloop_fixed<NW, NO, CPOL, 6>(ws, ao, q0, src, gs, lane, acc); break;
+    default: oloop_rolled<NW, NO, CPOL>(ws, ao, q0, q1, src, gs, lane, acc); break;
+  }
+}
+
+// Sum of the 4 columns of each token (lanes 4t .. 4t+3), left in lane 4t:
+// (c0 + c1) + (c2 + c3), with c = 2*part + g.
+__device__ __forceinline__ float col4_sum(float v) {
+  v += dpp_f<0xB1>(v);  // lane ^ 1
+  v += dpp_f<0x4E>(v);  // lane ^ 2
+  return v;
+}
+
+// Grouped gate/up on octets: one workgroup of 4 waves per (2 units of F,
+// item of <= 8 rows): wave w streams unit 2*blockIdx.x + w%2 (gate and up,
+// 32 rows each) over K-half w/2; the K-halves meet in LDS; then each
+// 32-lane half of a wave takes one (unit, token), applies clamp + SwiGLU and
+// writes the unit's Q8_0 h block of that token.  grid (F/64, item capacity).
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_gate_up_o(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
+                 const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
+                 int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
+                 float *__restrict__ htap) {
+  __shared__ __align__(16) float red[4][2][8][MOE_UNIT];  // [wave][gate/up][token][row]
+  if ((int)blockIdx.y >= items[0]) return;
+  const int4 it = item_of(items, blockIdx.y);
+  const int NQ = H / 128, NQ4 = moe_nq4(NQ), U = F / MOE_UNIT, tiles = F / MOE_TILE, KB = H / MOE_QK;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ul = wave & 1, kp = wave >> 1, P = T * k;
+  const int u = 2 * blockIdx.x + ul;
+  const int row0 = it.y, nt = it.z;
+  const bool shared = it.w != 0;
+  int q0, q1;
+  wave_quads(NQ, 2, kp, q0, q1);
+  const size_t t0 = (size_t)it.x * tiles + 2 * u;
+  const wstream ws[2] = {make_wstream32(w_g, t0, NQ4), make_wstream32(w_u, t0, NQ4)};
+  const aoff32 ao = make_aoff32(lane, NQ4);
+  const gsrc src = make_gsrc(xq, xd, T, KB);
+  gsel gs[1];
+  {
+    const int i = (lane & 31) >> 2;
+    int xr = -1;
+    if (i < nt) xr = shared ? row0 + i - P : perm[row0 + i] / k;
+    gs[0] = make_gsel32(lane, xr, KB);
+  }
+  f32x16_t acc[1][2];
+  oloop_any<2, 1, 0>(ws, ao, q0, q1, src, gs, lane, acc);
+  const int n = lane & 31, gb = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const float v = col4_sum(acc[0][i][e]);
+      if ((n & 3) == 0) red[wave][i][n >> 2][8 * (e >> 2) + 4 * gb + (e & 3)] = v;
+    }
+  __syncthreads();
+  // (unit, token) c = 8*round + 2*wave + half: unit ul2 = c / 8, token c % 8
+#pragma unroll
+  for (int round = 0; round < 2; round++) {
+    const int c = 8 * round + 2 * wave + (lane >> 5);
+    const int ul2 = c >> 3, t = c & 7, j = lane & 31;
+    const bool live = t < nt;
+    // waves ul2 (K-half 0) and ul2 + 2 (K-half 1) hold this unit
+    const float gsum = red[ul2][0][t][j] + red[ul2 + 2][0][t][j];
+    const float usum = red[ul2][1][t][j] + red[ul2 + 2][1][t][j];
+    const float h = live ? swiglu(gsum, usum, clamp) : 0.0f;
+    const int hrow = row0 + (live ? t : 0), uu = 2 * blockIdx.x + ul2;
+    h_unit_store(h, live, hs + ((size_t)hrow * U + uu) * MOE_XSW, hd + (size_t)hrow * U + uu, lane);
+    if (htap && live) htap[(size_t)hrow * F + (size_t)uu * MOE_UNIT + j] = h;
+  }
+}
+
+// Grouped down on octets: each wave streams one 32-row tile of H of the
+// item's down matrix over all of F against the item's (<= 8) h rows;
+// y[r][H] = (row . h[r]) * wts[perm[r]] (routed) or * 1 (shared).
+// grid (H/128, item capacity), 4 waves.
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_down_o(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+              int n_rows, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
+              const float *__restrict__ wts, int F, int H, float *__restrict__ y) {
+  if ((int)blockIdx.y >= items[0]) return;
+  const int4 it = item_of(items, blockIdx.y);
+  const int NQ = F / 128, NQ4 = moe_nq4(NQ), tiles = H / MOE_TILE, KB = F / MOE_QK;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t32 = blockIdx.x * 4 + wave;  // 32-row tile of H
+  const int row0 = it.y, nt = it.z;
+  const bool shared = it.w != 0;
+  const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
+  const aoff32 ao = make_aoff32(lane, NQ4);
+  const gsrc src = make_gsrc(hs, hd, n_rows, KB);
+  const int n = lane & 31, gb = lane >> 5, t = n >> 2;
+  gsel gs[1] = {make_gsel32(lane, t < nt ? row0 + t : -1, KB)};
+  f32x16_t acc[1][1];
+  oloop_any<1, 1, 0>(ws, ao, 0, NQ, src, gs, lane, acc);
+  const bool live = t < nt;
+  const int r = row0 + (live ? t : 0);
+  const float wt = (live && !shared) ? wts[perm[r]] : 1.0f;
+  float v[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    v[e] = col4_sum(acc[0][0][e]);
+    if (!shared) v[e] = __fmul_rn(v[e], wt);
+  }
+  if ((n & 3) == 0 && live) {
+    float *dst = y + (size_t)r * H + (size_t)t32 * 32 + 4 * gb;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  }
+}

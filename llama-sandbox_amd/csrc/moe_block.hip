@@ -537,13 +537,11 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   return MOE_OK;
 }
 
-// Token pairs of the largest work item of the grouped chain (items hold up
-// to 2 * NPMAX grouped rows of one expert).
-static int pick_npmax(int T) { return T <= 4 ? 2 : 4; }
+// The grouped chain runs token pairs on the 16x16x128 MFMA for T <= 4
+// (items of at most 4 rows: NPMAX = 2 pairs), token octets on the 32x32x64
+// MFMA above that (items of at most 8 rows).
+static bool use_octets(int T) { return T > 4; }
 
-// The grouped chain for T > 1, four launches: k_group (grouping, work items,
-// and Q8_0 of x by its extra workgroups) -> gate/up per (32-row unit, item)
-// -> down per (128 rows of H, item) -> combine in slot order.
 static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
                                   int T, float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
@@ -553,7 +551,8 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   if (P > MOE_GROUP_MAX_PAIRS || E > MOE_GROUP_MAX_E)
     return fail(c, MOE_ERR_UNSUPPORTED, "grouped: more than %d pairs or %d experts", MOE_GROUP_MAX_PAIRS,
                 MOE_GROUP_MAX_E);
-  const int NPM = pick_npmax(T), BT = 2 * NPM;
+  const bool oct = use_octets(T);
+  const int BT = oct ? 8 : 4;
   scratch &s = c->sc;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
   float *htap = c->taps ? s.htap : nullptr;
@@ -567,9 +566,8 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   {
     prof_scope pg(c, K_GU_GROUPED, st);
 #define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
-    const dim3 g(F / MOE_UNIT, cap), b(256);
-    if (NPM == 4) hipLaunchKernelGGL(k_gate_up_g<4>, g, b, 0, st, MOE_GU_ARGS);
-    else hipLaunchKernelGGL(k_gate_up_g<2>, g, b, 0, st, MOE_GU_ARGS);
+    if (oct) hipLaunchKernelGGL(k_gate_up_o, dim3(F / (2 * MOE_UNIT), cap), dim3(256), 0, st, MOE_GU_ARGS);
+    else hipLaunchKernelGGL(k_gate_up_g<2>, dim3(F / MOE_UNIT, cap), dim3(256), 0, st, MOE_GU_ARGS);
 #undef MOE_GU_ARGS
   }
   s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
@@ -577,9 +575,9 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   {
     prof_scope pd(c, K_DOWN_GROUPED, st);
 #define MOE_DN_ARGS L.m[T_DOWN].w, s.hq, s.hd, P + T, items, perm, wts, F, H, s.y
-    const dim3 g(ceil_div(H / (2 * MOE_TILE), MOE_DG_WAVES), cap), b(64 * MOE_DG_WAVES);
-    if (NPM == 4) hipLaunchKernelGGL(k_down_g<4>, g, b, 0, st, MOE_DN_ARGS);
-    else hipLaunchKernelGGL(k_down_g<2>, g, b, 0, st, MOE_DN_ARGS);
+    if (oct) hipLaunchKernelGGL(k_down_o, dim3(H / 128, cap), dim3(256), 0, st, MOE_DN_ARGS);
+    else hipLaunchKernelGGL(k_down_g<2>, dim3(ceil_div(H / (2 * MOE_TILE), MOE_DG_WAVES), cap),
+                            dim3(64 * MOE_DG_WAVES), 0, st, MOE_DN_ARGS);
 #undef MOE_DN_ARGS
   }
   {

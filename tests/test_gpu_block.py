@@ -74,7 +74,9 @@ def check_block(oracle, L, blk, shape, x, ids, wts, got, what, n_threads=16):
     """Parity of one forward, in two stages.
 
     1. gate/up + clamp + SwiGLU: the GPU's h against the oracle's h, max|dh|
-       <= 3e-5 * max|h| per row (only the f32 summation order differs).
+       <= 2e-4 * max|h| per row (only the f32 summation order differs; the
+       bound leaves room for cancellation in the gate/up sums, which is
+       large when the clamp is active).
     2. The output, max|d| <= TOL * RMS: against the oracle run end to end
        for every token whose Q8_0(h) codes come out identical on both sides,
        and for a token where an h value sits so close to a Q8_0 rounding
@@ -90,7 +92,8 @@ def check_block(oracle, L, blk, shape, x, ids, wts, got, what, n_threads=16):
         b2 = b.reshape(-1, b.shape[-1]).astype(np.float64)
         scale = np.maximum(np.abs(b2).max(axis=1, keepdims=True), 1e-30)
         worst = float((np.abs(a2 - b2) / scale).max())
-        assert worst <= 3e-5, f"{what} {nm}: max|dh|/max|h| = {worst:.3e}"
+        say(f"{what} {nm}: max|dh|/max|h| = {worst:.3e}")
+        assert worst <= 2e-4, f"{what} {nm}: max|dh|/max|h| = {worst:.3e}"
     T = x.shape[0]
     flips = []
     for t in range(T):
@@ -213,7 +216,7 @@ def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
 
 # ---- clamp-active (the reference's synthetic weights never trigger the clamp) ---------
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 7])
 def test_clamp_active(blk, torch_dev, oracle, T):
     shape = wl.LayerShape(hidden=1024, ffn=512, n_expert=16, n_used=4, has_shared=True,
                           route_mode=wl.ROUTE_SIGMOID, clamp=0.75)
@@ -228,7 +231,7 @@ def test_clamp_active(blk, torch_dev, oracle, T):
         unclamped = oracle_layer(oracle, shape, 55, 7, ids, clamp=0.0, e_lo=128, e_span=3).forward(
             x, ids, wts, taps=True)
         assert np.abs(unclamped["h"]).max() > 4 * np.abs(ref["h"]).max()  # the clamp binds
-        assert_rms_close(got, ref["out"], what="clamp")
+        check_block(oracle, L, blk, shape, x, ids, wts, got, f"clamp T{T}")
     finally:
         blk.release_layer(7)
 
