@@ -216,7 +216,7 @@ def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
 
 # ---- clamp-active (the reference's synthetic weights never trigger the clamp) ---------
 
-@pytest.mark.parametrize("T", [1, 3, 7])
+@pytest.mark.parametrize("T", [1, 3, 7, 40])
 def test_clamp_active(blk, torch_dev, oracle, T):
     shape = wl.LayerShape(hidden=1024, ffn=512, n_expert=16, n_used=4, has_shared=True,
                           route_mode=wl.ROUTE_SIGMOID, clamp=0.75)
