@@ -389,6 +389,7 @@ __device__ __forceinline__ void kloop_any(kring<NW, D> &r, const wstream (&ws)[N
                                           const bsel (&bs)[NP], const uint32_t *xs, const float *dy, int lane,
                                           f32x4_t (&acc)[NP][NW]) {
   switch (q1 - q0) {
+    case 56: kloop_fixed<NW, NP, D, 56>(r, ws, q0, bs, xs, dy, lane, acc); break;
     case 28: kloop_fixed<NW, NP, D, 28>(r, ws, q0, bs, xs, dy, lane, acc); break;
     case 16: kloop_fixed<NW, NP, D, 16>(r, ws, q0, bs, xs, dy, lane, acc); break;
     default: kloop<NW, NP, D>(r, ws, q0, q1, bs, xs, dy, lane, acc); break;
@@ -601,6 +602,78 @@ void k_gate_up(
     }
     __syncthreads();
   }
+}
+
+// Decode gate/up with equal work per CU.  The step's gate/up work is
+// S*U*4 one-stream wave tasks (slot s, 32-row unit u, matrix gate/up, 16-row
+// tile), each streaming its tile over all of K; MOE_BAL_WAVES of them per
+// workgroup (for V3: 2304 tasks = 256 workgroups of 9 waves, one per CU, all
+// waves of a CU the same age).  x is quantized once per workgroup into LDS.
+// The 4 tasks of a unit may sit in different workgroups: each writes its 16
+// row sums with coherent stores, then counts itself on the unit's ticket;
+// the 4th applies clamp + SwiGLU, writes the unit's Q8_0 h block and resets
+// the ticket (so every launch starts from zero, graph replays included).
+// Nothing waits.  grid ceil(S*U*4 / MOE_BAL_WAVES), 64*MOE_BAL_WAVES threads.
+#define MOE_BAL_WAVES 9
+#define MOE_BAL_RING 4  // quads in a wave's load ring (8 measured slower)
+
+__global__ __launch_bounds__(64 * MOE_BAL_WAVES) void k_gate_up_bal(
+    const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const float *__restrict__ x,
+    const int32_t *__restrict__ ids, int k, int E, int S, int F, int H, float clamp, float *__restrict__ part,
+    int *__restrict__ tick, uint32_t *__restrict__ hs, float *__restrict__ hd, float *__restrict__ htap) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int NQ = H / 128, NQ4 = moe_nq4(NQ), KB = H / MOE_QK, U = F / MOE_UNIT, tiles = F / MOE_TILE;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int task = blockIdx.x * MOE_BAL_WAVES + wave, n_tasks = S * U * 4;
+  const bool active = task < n_tasks;
+  const int tt = active ? task : 0;
+  const int ti = tt & 1, mi = (tt >> 1) & 1, unit = tt >> 2;  // unit = s*U + u
+  const int s = unit / U, u = unit % U;
+  uint32_t *xs = lds;
+  float *dy = reinterpret_cast<float *>(lds + 4 + (size_t)KB * MOE_XSW);
+  int e = s < k ? ids[s] : E;
+  const bool valid = s >= k || (unsigned)e < (unsigned)E;  // an out-of-range id reads nothing, yields 0
+  e = valid ? e : 0;
+  const wstream ws[1] = {make_wstream(mi ? w_u : w_g, (size_t)e * tiles + 2 * u + ti, NQ4)};
+  kring<1, MOE_BAL_RING> ring;
+  if (active) kloop_prime<1, MOE_BAL_RING>(ring, ws, 0, NQ, lane);
+  if (threadIdx.x < 4) xs[threadIdx.x] = 0u;
+  stage_quant(x, KB, xs + 4, dy, threadIdx.x, 64 * MOE_BAL_WAVES);
+  __syncthreads();
+  if (!active) return;
+  const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
+  f32x4_t acc[1][1];
+  kloop_any<1, 1, MOE_BAL_RING>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
+  const int gb = lane >> 4, tp = (lane >> 3) & 1;
+  float *pu = part + (size_t)unit * 4 * MOE_TILE;  // [matrix][tile][16 rows]
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    const float v = col8_sum(acc[0][0][r]);
+    if ((lane & 7) == 0 && tp == 0)
+      __hip_atomic_store(reinterpret_cast<uint32_t *>(pu + (mi * 2 + ti) * MOE_TILE + 4 * gb + r),
+                         __builtin_bit_cast(uint32_t, v), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the row sums are complete before they are counted
+  int old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(tick + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  old = __builtin_amdgcn_readfirstlane(old);
+  if (old != 3) return;
+  // the unit's 4th task: lanes 0-31 = rows of the unit (tile j/16)
+  const int j = lane & 31, tj = j >> 4, rr = j & 15;
+  const bool live = lane < 32;
+  const float g = __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t *>(pu + tj * MOE_TILE + rr),
+                                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const float up = __builtin_bit_cast(float, __hip_atomic_load(
+                                                 reinterpret_cast<const uint32_t *>(pu + (2 + tj) * MOE_TILE + rr),
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  const float h = live && valid ? swiglu(g, up, clamp) : 0.0f;
+  h_unit_store(h, live, hs + ((size_t)s * U + u) * MOE_XSW, hd + (size_t)s * U + u, lane);
+  if (htap && live) htap[(size_t)s * F + (size_t)u * MOE_UNIT + j] = h;
+  if (lane == 0) __hip_atomic_store(tick + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+static inline size_t gate_up_bal_lds_bytes(int H) {
+  return ((size_t)4 + (size_t)(H / MOE_QK) * (MOE_XSW + 1)) * 4;
 }
 
 // Decode down with the top-k combine (T == 1).  One workgroup per 16-row tile

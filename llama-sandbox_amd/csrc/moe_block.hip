@@ -50,6 +50,9 @@ struct scratch {
   float *htap = nullptr;                           // [P+T][F]
   float *y = nullptr;                              // [P+T][H]
   uint32_t *xq = nullptr; float *xd = nullptr;     // staged x of the grouped chain: [T][H/32][16] dwords, [T][H/32]
+  // balanced decode gate/up: per-task row sums [16 slots][F/32][4][16] and
+  // per-unit tickets (zeroed here once, left at zero by every launch)
+  float *part = nullptr; int *tick = nullptr;
   int32_t *grp = nullptr;                          // grouping workspace
   size_t grp_words = 0;
   // split-K decode: chunk partial sums and per-unit tickets (the tickets are
@@ -191,7 +194,8 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 // scratch
 
 static void scratch_free(scratch &s) {
-  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.grp, s.x_in, s.ids_in, s.wts_in, s.out_buf};
+  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.part, s.tick, s.grp, s.x_in, s.ids_in, s.wts_in,
+                  s.out_buf};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   s = scratch();
@@ -215,6 +219,9 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipMalloc(&s.y, R * H * 4));
   HIPC(c, hipMalloc(&s.xq, (size_t)T * (H / 32) * 64));
   HIPC(c, hipMalloc(&s.xd, (size_t)T * (H / 32) * 4));
+  HIPC(c, hipMalloc(&s.part, (size_t)16 * (F / 32) * 4 * 16 * 4));
+  HIPC(c, hipMalloc(&s.tick, (size_t)16 * (F / 32) * 4));
+  HIPC(c, hipMemset(s.tick, 0, (size_t)16 * (F / 32) * 4));
   s.grp_words = group_ws_words(T, k, E);
   HIPC(c, hipMalloc(&s.grp, s.grp_words * 4));
   HIPC(c, hipMalloc(&s.x_in, (size_t)T * H * 4));
@@ -523,15 +530,21 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
     return forward_grouped(c, L, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
   {
     prof_scope pg(c, K_GU_DECODE, st);
-    launch_gate_up_decode(dim3(F / MOE_UNIT, S), st, L, x, ids, shared, s.hq, s.hd, htap);
+    if (gate_up_bal_lds_bytes(H) <= 65536) {
+      const int n_wg = ceil_div((long)S * (F / MOE_UNIT) * 4, MOE_BAL_WAVES);
+      hipLaunchKernelGGL(k_gate_up_bal, dim3(n_wg), dim3(64 * MOE_BAL_WAVES), gate_up_bal_lds_bytes(H), st,
+                         L.m[T_GATE].w, L.m[T_UP].w, x, ids, k, E, S, F, H, d.clamp, s.part, s.tick, s.hq, s.hd,
+                         htap);
+    } else {
+      launch_gate_up_decode(dim3(F / MOE_UNIT, S), st, L, x, ids, shared, s.hq, s.hd, htap);
+    }
   }
   s.h_rows = htap ? (size_t)S : 0;
   s.last_F = F;
   {
     prof_scope pd(c, K_DOWN_DECODE, st);
     hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].w, s.hq, s.hd, ids,
-                       wts, k, E, S, F, H,
-                       per_slot ? 1 : 0, out);
+                       wts, k, E, S, F, H, per_slot ? 1 : 0, out);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
