@@ -719,3 +719,129 @@ void k_down_o(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, 
       *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   }
 }
+
+// ===========================================================================
+// Octet B operand staged in LDS (the grouped down kernel).  Every wave of a
+// down workgroup multiplies the same item's h rows, so the workgroup copies
+// them into LDS once, already in MFMA lane order: step s (blocks 2s, 2s+1)
+// is 64 lanes x 16 bytes, lane n + 32*gb = column n (token n/4, part
+// (n/2)%2, block 2s + n%2), bytes 16*gb .. 16*gb+15 of that block's part;
+// scales d[s][token][n%2].  A lane's B read is one ds_read_b128 of 16
+// consecutive bytes per step (the 64 lanes cover 1 KiB without bank
+// conflicts), and the vector-memory unit only carries the weights.
+
+// LDS bytes for KB blocks per row (KB even): digits, then scales.
+__host__ __device__ __forceinline__ size_t octet_lds_bytes(int KB) {
+  return (size_t)(KB / 2) * 64 * 16 + (size_t)(KB / 2) * 16 * 4;
+}
+
+// Copy the nt (<= 8) staged rows row0 .. of KB blocks into that layout;
+// columns of absent tokens get zeros.  tid / nthr: this thread among nthr.
+__device__ __forceinline__ void stage_octet_lds(const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+                                                int row0, int nt, int KB, u32x4_t *bl, float *dl, int tid,
+                                                int nthr) {
+  const u32x4_t *src = reinterpret_cast<const u32x4_t *>(hs + (size_t)row0 * KB * MOE_XSW);
+  const int n16 = 8 * KB * 4;  // 16-byte chunks of 8 rows
+#pragma unroll 4
+  for (int c = tid; c < n16; c += nthr) {
+    const int t = c / (4 * KB), w = c - t * 4 * KB, b = w >> 2, sub = w & 3;
+    const int L = 32 * (sub & 1) + 4 * t + 2 * (sub >> 1) + (b & 1);
+    bl[(b >> 1) * 64 + L] = t < nt ? src[c] : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  for (int c = tid; c < 8 * KB; c += nthr) {
+    const int t = c / KB, b = c - t * KB;
+    dl[((b >> 1) * 8 + t) * 2 + (b & 1)] = t < nt ? hd[(size_t)(row0 + t) * KB + b] : 0.0f;
+  }
+}
+
+// Ring of the LDS-B octet loop: weights of 4 quads (3 ahead), B of 2 quads
+// (1 ahead, from LDS), exponent dwords of NG groups.
+template <int NW, int NG>
+struct oring_l {
+  wq32<NW> w[4];
+  bq32<1> b[2];
+  uint32_t sc[NG][NW][2];
+};
+
+__device__ __forceinline__ void load_bq32_lds(bq32<1> &b, const u32x4_t *bl, const float *dl, int lane, int dlo,
+                                              int q) {
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    b.v[0][j] = bl[(2 * q + j) * 64 + lane];
+    b.d[0][j] = dl[(2 * q + j) * 16 + dlo];
+  }
+}
+
+// Weights and exponents of the first quads, issued before the B staging.
+template <int NW, int NG, int CPOL>
+__device__ __forceinline__ void oprime_l(oring_l<NW, NG> &r, const wstream (&ws)[NW], const aoff32 &ao, int NQW) {
+  load_sc32<NW>(r.sc[0], ws, ao, 0);
+  load_wq32<NW, CPOL>(r.w[0], ws, ao, 0);
+  if (NQW > 1) load_wq32<NW, CPOL>(r.w[1], ws, ao, 1);
+  if (NQW > 2) load_wq32<NW, CPOL>(r.w[2], ws, ao, 2);
+}
+
+template <int QL, int NQW, int NW, int NG, int CPOL>
+__device__ __forceinline__ void olfixed_from(oring_l<NW, NG> &r, const wstream (&ws)[NW], const aoff32 &ao,
+                                             const u32x4_t *bl, const float *dl, int lane, int dlo, bool upper,
+                                             int sb, f32x16_t (&acc)[1][NW]) {
+  if constexpr (QL < NQW) {
+    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<NW>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
+    if constexpr (QL + 1 < NQW) load_bq32_lds(r.b[(QL + 1) & 1], bl, dl, lane, dlo, QL + 1);
+    if constexpr (QL + 3 < NQW) load_wq32<NW, CPOL>(r.w[(QL + 3) & 3], ws, ao, QL + 3);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    quad_mma32<QL & 3, NW, 1>(r.w[QL & 3], r.sc[QL >> 2], r.b[QL & 1], upper, sb, acc);
+    olfixed_from<QL + 1, NQW, NW, NG, CPOL>(r, ws, ao, bl, dl, lane, dlo, upper, sb, acc);
+  }
+}
+
+// Grouped down on octets with B in LDS: k_down_o's work split (each wave one
+// 32-row tile of H over all of F, y = (row . h) * router weight), NQ = F/128
+// in {6, 8, 16, 28}.  grid (H/128, item capacity), 4 waves, LDS
+// octet_lds_bytes(F/32).
+template <int NQ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_down_ol(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+               int n_rows, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
+               const float *__restrict__ wts, int F, int H, float *__restrict__ y) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  if ((int)blockIdx.y >= items[0]) return;
+  const int4 it = item_of(items, blockIdx.y);
+  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, KB = NQ * 4;
+  const int tiles = H / MOE_TILE;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t32 = blockIdx.x * 4 + wave;  // 32-row tile of H
+  const int row0 = it.y, nt = it.z;
+  const bool shared = it.w != 0;
+  const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
+  const aoff32 ao = make_aoff32(lane, NQ4);
+  oring_l<1, NG> r;
+  oprime_l<1, NG, 0>(r, ws, ao, NQ);
+  u32x4_t *bl = reinterpret_cast<u32x4_t *>(lds);
+  float *dl = reinterpret_cast<float *>(lds + (KB / 2) * 64 * 4);
+  stage_octet_lds(hs, hd, row0, nt, KB, bl, dl, threadIdx.x, 256);
+  __syncthreads();
+  const int n = lane & 31, gb = lane >> 5, t = n >> 2;
+  const int dlo = t * 2 + (n & 1);
+  f32x16_t acc[1][1];
+#pragma unroll
+  for (int e = 0; e < 16; e++) acc[0][0][e] = 0.0f;
+  load_bq32_lds(r.b[0], bl, dl, lane, dlo, 0);
+  olfixed_from<0, NQ, 1, NG, 0>(r, ws, ao, bl, dl, lane, dlo, lane_upper32(lane), lane_bscale32(lane), acc);
+  const bool live = t < nt;
+  const int rr = row0 + (live ? t : 0);
+  const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
+  float v[16];
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    v[e] = col4_sum(acc[0][0][e]);
+    if (!shared) v[e] = __fmul_rn(v[e], wt);
+  }
+  if ((n & 3) == 0 && live) {
+    float *dst = y + (size_t)rr * H + (size_t)t32 * 32 + 4 * gb;
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+  }
+}

@@ -588,7 +588,13 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   {
     prof_scope pd(c, K_DOWN_GROUPED, st);
 #define MOE_DN_ARGS L.m[T_DOWN].w, s.hq, s.hd, P + T, items, perm, wts, F, H, s.y
-    if (oct) hipLaunchKernelGGL(k_down_o, dim3(H / 128, cap), dim3(256), 0, st, MOE_DN_ARGS);
+    const dim3 gdo(H / 128, cap);
+    const size_t lo = octet_lds_bytes(F / MOE_QK);
+    if (oct && F == 128 * 16) hipLaunchKernelGGL(k_down_ol<16>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
+    else if (oct && F == 128 * 6) hipLaunchKernelGGL(k_down_ol<6>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
+    else if (oct && F == 128 * 8) hipLaunchKernelGGL(k_down_ol<8>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
+    else if (oct && F == 128 * 28) hipLaunchKernelGGL(k_down_ol<28>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
+    else if (oct) hipLaunchKernelGGL(k_down_o, gdo, dim3(256), 0, st, MOE_DN_ARGS);
     else hipLaunchKernelGGL(k_down_g<2>, dim3(ceil_div(H / (2 * MOE_TILE), MOE_DG_WAVES), cap),
                             dim3(64 * MOE_DG_WAVES), 0, st, MOE_DN_ARGS);
 #undef MOE_DN_ARGS
