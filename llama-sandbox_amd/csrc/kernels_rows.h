@@ -676,6 +676,102 @@ static inline size_t gate_up_bal_lds_bytes(int H) {
   return ((size_t)4 + (size_t)(H / MOE_QK) * (MOE_XSW + 1)) * 4;
 }
 
+// The same work split with most units meeting in LDS, for shapes where the
+// S*U*4 tasks are exactly 9 per workgroup and G % 4 == 0 (V3: G = 256):
+// waves 0-7 of workgroup b run the 8 tasks of units 2b and 2b+1, whose row
+// sums meet in LDS (no ticket); wave 8 runs one task of the last G/4 units
+// (task b % 4 of unit 2G + b/4), which meet through coherent stores and the
+// ticket as in k_gate_up_bal.  Wave 8 streams with a ring of 8 quads (7 in
+// flight instead of 3), so it takes a larger share of the CU's bandwidth,
+// finishes first, and its ticket chain runs while the other waves stream.
+// grid G, 64*MOE_BAL_WAVES threads, LDS gate_up_bal2_lds_bytes(H).
+#define MOE_BAL2_RING 8
+
+__global__ __launch_bounds__(64 * MOE_BAL_WAVES) void k_gate_up_bal2(
+    const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const float *__restrict__ x,
+    const int32_t *__restrict__ ids, int k, int E, int S, int F, int H, float clamp, float *__restrict__ part,
+    int *__restrict__ tick, uint32_t *__restrict__ hs, float *__restrict__ hd, float *__restrict__ htap) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  const int NQ = H / 128, NQ4 = moe_nq4(NQ), KB = H / MOE_QK, U = F / MOE_UNIT, tiles = F / MOE_TILE;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int G = gridDim.x;
+  const bool local = wave < 8;
+  const int unit = local ? 2 * blockIdx.x + (wave >> 2) : 2 * G + (blockIdx.x >> 2);  // unit = s*U + u
+  const int tq = local ? (wave & 3) : (blockIdx.x & 3);                                  // matrix*2 + tile
+  const int ti = tq & 1, mi = tq >> 1;
+  const int s = unit / U, u = unit % U;
+  uint32_t *xs = lds;
+  float *dy = reinterpret_cast<float *>(lds + 4 + (size_t)KB * MOE_XSW);
+  float *red = dy + KB;  // [8 waves][16 rows]
+  int e = s < k ? ids[s] : E;
+  const bool valid = s >= k || (unsigned)e < (unsigned)E;  // an out-of-range id reads nothing, yields 0
+  e = valid ? e : 0;
+  const wstream ws[1] = {make_wstream(mi ? w_u : w_g, (size_t)e * tiles + 2 * u + ti, NQ4)};
+  kring<1, MOE_BAL_RING> ring;
+  kring<1, MOE_BAL2_RING> ring8;
+  if (local) kloop_prime<1, MOE_BAL_RING>(ring, ws, 0, NQ, lane);
+  else kloop_prime<1, MOE_BAL2_RING>(ring8, ws, 0, NQ, lane);
+  if (threadIdx.x < 4) xs[threadIdx.x] = 0u;
+  stage_quant(x, KB, xs + 4, dy, threadIdx.x, 64 * MOE_BAL_WAVES);
+  __syncthreads();
+  const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
+  f32x4_t acc[1][1];
+  if (local) kloop_any<1, 1, MOE_BAL_RING>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
+  else kloop_any<1, 1, MOE_BAL2_RING>(ring8, ws, 0, NQ, bs, xs, dy, lane, acc);
+  const int gb = lane >> 4, tp = (lane >> 3) & 1;
+  if (local) {
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float v = col8_sum(acc[0][0][r]);
+      if ((lane & 7) == 0 && tp == 0) red[wave * MOE_TILE + 4 * gb + r] = v;
+    }
+  } else {
+    float *pu = part + (size_t)unit * 4 * MOE_TILE;  // [matrix][tile][16 rows]
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      const float v = col8_sum(acc[0][0][r]);
+      if ((lane & 7) == 0 && tp == 0)
+        __hip_atomic_store(reinterpret_cast<uint32_t *>(pu + tq * MOE_TILE + 4 * gb + r), __builtin_bit_cast(uint32_t, v),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // the row sums are complete before they are counted
+    int old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(tick + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == 3) {
+      // the unit's 4th task: lanes 0-31 = rows of the unit (tile j/16)
+      const int j = lane & 31, tj = j >> 4, rr = j & 15;
+      const bool live = lane < 32;
+      const float g = __builtin_bit_cast(float, __hip_atomic_load(reinterpret_cast<const uint32_t *>(pu + tj * MOE_TILE + rr),
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      const float up = __builtin_bit_cast(float, __hip_atomic_load(
+                                                     reinterpret_cast<const uint32_t *>(pu + (2 + tj) * MOE_TILE + rr),
+                                                     __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      const float h = live && valid ? swiglu(g, up, clamp) : 0.0f;
+      h_unit_store(h, live, hs + ((size_t)s * U + u) * MOE_XSW, hd + (size_t)s * U + u, lane);
+      if (htap && live) htap[(size_t)s * F + (size_t)u * MOE_UNIT + j] = h;
+      if (lane == 0) __hip_atomic_store(tick + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (wave == 0) {
+    // half hu of the wave: unit 2b + hu, lane j of the half = row j (tile j/16)
+    const int hu = lane >> 5, j = lane & 31, tj = j >> 4, rr = j & 15;
+    const int un = 2 * blockIdx.x + hu, s2 = un / U, u2 = un % U;
+    const float g = red[(4 * hu + tj) * MOE_TILE + rr];
+    const float up = red[(4 * hu + 2 + tj) * MOE_TILE + rr];
+    int e2 = s2 < k ? ids[s2] : E;
+    const bool v2 = s2 >= k || (unsigned)e2 < (unsigned)E;
+    const float h = v2 ? swiglu(g, up, clamp) : 0.0f;
+    h_unit_store(h, true, hs + ((size_t)s2 * U + u2) * MOE_XSW, hd + (size_t)s2 * U + u2, lane);
+    if (htap) htap[(size_t)s2 * F + (size_t)u2 * MOE_UNIT + j] = h;
+  }
+}
+
+static inline size_t gate_up_bal2_lds_bytes(int H) {
+  return gate_up_bal_lds_bytes(H) + (size_t)8 * MOE_TILE * 4;
+}
+
 // Decode down with the top-k combine (T == 1).  One workgroup per 16-row tile
 // of H with one wave per slot (S <= 16): wave s streams the tile of its
 // expert's down matrix over all of F against its slot's staged h and scales

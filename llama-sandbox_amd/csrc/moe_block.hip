@@ -530,7 +530,12 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
     return forward_grouped(c, L, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
   {
     prof_scope pg(c, K_GU_DECODE, st);
-    if (gate_up_bal_lds_bytes(H) <= 65536) {
+    const long n_tasks = (long)S * (F / MOE_UNIT) * 4;
+    if (n_tasks % MOE_BAL_WAVES == 0 && (n_tasks / MOE_BAL_WAVES) % 4 == 0 && gate_up_bal2_lds_bytes(H) <= 65536) {
+      hipLaunchKernelGGL(k_gate_up_bal2, dim3(n_tasks / MOE_BAL_WAVES), dim3(64 * MOE_BAL_WAVES),
+                         gate_up_bal2_lds_bytes(H), st, L.m[T_GATE].w, L.m[T_UP].w, x, ids, k, E, S, F, H, d.clamp,
+                         s.part, s.tick, s.hq, s.hd, htap);
+    } else if (gate_up_bal_lds_bytes(H) <= 65536) {
       const int n_wg = ceil_div((long)S * (F / MOE_UNIT) * 4, MOE_BAL_WAVES);
       hipLaunchKernelGGL(k_gate_up_bal, dim3(n_wg), dim3(64 * MOE_BAL_WAVES), gate_up_bal_lds_bytes(H), st,
                          L.m[T_GATE].w, L.m[T_UP].w, x, ids, k, E, S, F, H, d.clamp, s.part, s.tick, s.hq, s.hd,
