@@ -530,8 +530,14 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
     return forward_grouped(c, L, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
   {
     prof_scope pg(c, K_GU_DECODE, st);
+    // the balanced kernels run one workgroup per CU: for shapes too small to
+    // fill half of the CUs that way (C1), the (unit, slot) grid spreads wider
     const long n_tasks = (long)S * (F / MOE_UNIT) * 4;
-    if (n_tasks % MOE_BAL_WAVES == 0 && (n_tasks / MOE_BAL_WAVES) % 4 == 0 && gate_up_bal2_lds_bytes(H) <= 65536) {
+    const bool wide = n_tasks / MOE_BAL_WAVES >= c->n_cu / 2;
+    if (!wide) {
+      launch_gate_up_decode(dim3(F / MOE_UNIT, S), st, L, x, ids, shared, s.hq, s.hd, htap);
+    } else if (n_tasks % MOE_BAL_WAVES == 0 && (n_tasks / MOE_BAL_WAVES) % 4 == 0 &&
+               gate_up_bal2_lds_bytes(H) <= 65536) {
       hipLaunchKernelGGL(k_gate_up_bal2, dim3(n_tasks / MOE_BAL_WAVES), dim3(64 * MOE_BAL_WAVES),
                          gate_up_bal2_lds_bytes(H), st, L.m[T_GATE].w, L.m[T_UP].w, x, ids, k, E, S, F, H, d.clamp,
                          s.part, s.tick, s.hq, s.hd, htap);
