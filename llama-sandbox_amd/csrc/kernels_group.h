@@ -189,3 +189,40 @@ __global__ __launch_bounds__(256) void k_combine(const float *__restrict__ y,
   if (shared) acc = __fadd_rn(acc, y[((size_t)P + t) * H + c]);
   out[i] = acc;
 }
+
+__device__ __forceinline__ float4 add4_rn(float4 a, float4 b) {
+  return make_float4(__fadd_rn(a.x, b.x), __fadd_rn(a.y, b.y), __fadd_rn(a.z, b.z), __fadd_rn(a.w, b.w));
+}
+
+// k_combine with one thread per 4 consecutive columns (H % 4 == 0, out
+// 16-byte aligned); grid ceil(T*H/4 / 256).
+__global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y,
+                                                 const int32_t *__restrict__ inv, int T, int k,
+                                                 int H, int shared, int per_slot,
+                                                 float *__restrict__ out) {
+  const int H4 = H / 4;
+  const size_t i = (size_t)blockIdx.x * 256u + threadIdx.x;
+  if (i >= (size_t)T * H4) return;
+  const int t = (int)(i / H4), c = (int)(i % H4);
+  const int P = T * k;
+  const float4 *y4 = reinterpret_cast<const float4 *>(y);
+  float4 *o4 = reinterpret_cast<float4 *>(out);
+  const float4 z = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  // a negative row marks a pair whose expert id was out of range: it contributes 0
+  if (per_slot) {
+    for (int s = 0; s < k; s++) {
+      const int r = inv ? inv[t * k + s] : t * k + s;
+      o4[((size_t)t * k + s) * H4 + c] = r >= 0 ? y4[(size_t)r * H4 + c] : z;
+    }
+    return;
+  }
+  const int r0 = inv ? inv[t * k] : t * k;
+  float4 acc = r0 >= 0 ? y4[(size_t)r0 * H4 + c] : z;
+#pragma unroll 8
+  for (int s = 1; s < k; s++) {
+    const int r = inv ? inv[t * k + s] : t * k + s;
+    acc = add4_rn(acc, r >= 0 ? y4[(size_t)r * H4 + c] : z);
+  }
+  if (shared) acc = add4_rn(acc, y4[((size_t)P + t) * H4 + c]);
+  o4[i] = acc;
+}

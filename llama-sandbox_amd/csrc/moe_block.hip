@@ -612,8 +612,12 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   }
   {
     prof_scope pc(c, K_COMBINE, st);
-    hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * H, 256)), dim3(256), 0, st, s.y, inv, T, k, H, shared,
-                       per_slot ? 1 : 0, out);
+    if ((reinterpret_cast<uintptr_t>(out) & 15) == 0)  // float4 stores
+      hipLaunchKernelGGL(k_combine4, dim3(ceil_div((long)T * (H / 4), 256)), dim3(256), 0, st, s.y, inv, T, k, H,
+                         shared, per_slot ? 1 : 0, out);
+    else
+      hipLaunchKernelGGL(k_combine, dim3(ceil_div((long)T * H, 256)), dim3(256), 0, st, s.y, inv, T, k, H, shared,
+                         per_slot ? 1 : 0, out);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;

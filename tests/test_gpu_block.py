@@ -216,6 +216,22 @@ def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
 
 # ---- clamp-active (the reference's synthetic weights never trigger the clamp) ---------
 
+@pytest.mark.parametrize("T", [3, 12])
+def test_grouped_output_not_16_byte_aligned(blk, torch_dev, oracle, c1, T):
+    """The slot combine stores 4 floats at a time when `out` is 16-byte
+    aligned and one at a time otherwise: both give the same bits."""
+    torch, dev = torch_dev
+    x, lg = wl.make_inputs(c1, T, 90 + T)
+    ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    aligned = run_block(blk, torch_dev, 1, x, ids, wts)
+    buf = torch.zeros(T * c1.hidden + 1, dtype=torch.float32, device=dev)
+    out = buf[1:].view(T, c1.hidden)
+    blk.forward(1, torch.from_numpy(x).to(dev), torch.from_numpy(ids).to(dev), torch.from_numpy(wts).to(dev), out)
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(out.cpu().numpy().view(np.int32), aligned.view(np.int32))
+    assert buf[0].item() == 0.0
+
+
 @pytest.mark.parametrize("T", [1, 3, 7, 40])
 def test_clamp_active(blk, torch_dev, oracle, T):
     shape = wl.LayerShape(hidden=1024, ffn=512, n_expert=16, n_used=4, has_shared=True,
