@@ -271,6 +271,35 @@ def test_c2_decode(blk, torch_dev, oracle, v3, seed):
     check_block(oracle, oracle_layer(oracle, v3, 202, 2, ids), blk, v3, x, ids, wts, got, "C2")
 
 
+def test_c2_decode_per_slot_and_no_shared(blk, torch_dev, oracle, v3):
+    """V3 decode without the shared expert: 8 slots, so the gate/up work (2048
+    tasks) is not 9 per workgroup and runs on k_gate_up_bal (every unit met
+    through a ticket) instead of k_gate_up_bal2.  Per-slot rows (the MUL
+    node) against the oracle's, and the slot sum without the shared expert
+    against the per-slot rows added in slot order on the host."""
+    x, lg = wl.make_inputs(v3, 1, 21)
+    ids, wts = oracle.route(lg, v3.n_used, v3.route_mode, norm=True)
+    say("C2 per-slot / no shared", ids.tolist())
+    ps = run_block(blk, torch_dev, 2, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
+    L = oracle_layer(oracle, v3, 202, 2, ids)
+    ref = L.forward(x, ids, wts, per_slot=True, taps=True)
+    hg, _ = gpu_h(blk, oracle, v3, ids, shared=False)
+    worst = float((np.abs(hg.astype(np.float64) - ref["h"]) / np.maximum(np.abs(ref["h"]).max(axis=-1, keepdims=True),
+                                                                          1e-30)).max())
+    say(f"C2 per-slot h: max|dh|/max|h| = {worst:.3e}")
+    assert worst <= 2e-4
+    for s in range(v3.n_used):
+        qa, da = oracle.quantize_q8_0(hg[0, s])
+        qb, db = oracle.quantize_q8_0(ref["h"][0, s])
+        if np.array_equal(qa, qb) and np.array_equal(da, db):
+            assert_rms_close(ps[0, s], ref["per_slot"][0, s], what=f"C2 slot {s}")
+    ns = run_block(blk, torch_dev, 2, x, ids, wts, flags=mb.MOE_FWD_NO_SHARED)
+    acc = ps[0, 0].copy()
+    for s in range(1, v3.n_used):
+        acc = (acc + ps[0, s]).astype(np.float32)
+    np.testing.assert_array_equal(ns[0].view(np.int32), acc.view(np.int32))
+
+
 def test_c2_route_forward_ids_bit_exact(blk, torch_dev, oracle, v3):
     torch, dev = torch_dev
     x, lg = wl.make_inputs(v3, 1, 3)
