@@ -27,11 +27,12 @@ static inline int group_item_cap(int T, int k, int E, int BT) {
 }
 
 // Workspace words for the grouped chain: counts[E] offsets[E+1] perm[P]
-// inv[P], then the item list (4-word header, 4 words per item) sized for
-// BT = 1.
+// inv[P], then two item lists (4-word header, 4 words per item), each sized
+// for BT = 1 (group_list_words).
+static inline size_t group_list_words(int T, int k, int E) { return 4 + 4 * (size_t)group_item_cap(T, k, E, 1); }
 static inline size_t group_ws_words(int T, int k, int E) {
   const size_t P = (size_t)T * k;
-  return (size_t)E + (E + 1) + 2 * P + 4 + 4 * (size_t)group_item_cap(T, k, E, 1);
+  return (size_t)E + (E + 1) + 2 * P + 2 * group_list_words(T, k, E);
 }
 
 // Lanes of the wave holding the same expert id as this lane (e >= 0, ids
@@ -57,6 +58,8 @@ __device__ __forceinline__ uint64_t same_id_lanes(int e, bool valid) {
 //   wc[w][e] turned into wave w's first row of expert e;
 //   pass 2: row of a pair = wc[w][e] + rank, so rows ascend in pair order
 //   within each expert (ggml mul_mat_id's order).
+// items2 != NULL: a second item list of at most BT2 rows per item, the same
+// way (the gate/up and down kernels of a call may take different item sizes).
 // Workgroups 1..: Q8_0 of x (T rows of H, flat n_xblocks blocks) into the
 // staged format of the grouped kernels (xq, xd), MOE_GROUP_QBLOCKS blocks
 // each; none when xq is NULL.
@@ -65,7 +68,8 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
                                                 int32_t *__restrict__ offsets,
                                                 int32_t *__restrict__ perm, int32_t *__restrict__ inv,
                                                 int32_t *__restrict__ items, const float *__restrict__ x,
-                                                int n_xblocks, uint32_t *__restrict__ xq, float *__restrict__ xd) {
+                                                int n_xblocks, uint32_t *__restrict__ xq, float *__restrict__ xd,
+                                                int BT2, int32_t *__restrict__ items2) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   if (blockIdx.x > 0) {
     const int b0 = (blockIdx.x - 1) * MOE_GROUP_QBLOCKS;
@@ -74,7 +78,7 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     return;
   }
   __shared__ uint16_t wc[16][MOE_GROUP_MAX_E];  // per-wave counts, then per-wave first rows (< 2^16)
-  __shared__ int32_t wsum[16], wsumi[16], tot[1];
+  __shared__ int32_t wsum[16], wsumi[16], wsumi2[16], tot[2];
   const int PW = ((P + 15) / 16 + 63) & ~63;    // pairs per wave, whole steps of 64
   const int p_lo = wave * PW, p_hi = p_lo + PW < P ? p_lo + PW : P;
   for (int i = tid; i < 16 * MOE_GROUP_MAX_E; i += 1024) (&wc[0][0])[i] = 0;
@@ -93,26 +97,30 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
   if (tid < E)
     for (int w = 0; w < 16; w++) c += wc[w][tid];
   const int ni = items ? (c + BT - 1) / BT : 0;
-  int v = c, vi = ni;
+  const int ni2 = items2 ? (c + BT2 - 1) / BT2 : 0;
+  int v = c, vi = ni, vi2 = ni2;
 #pragma unroll
   for (int off = 1; off < 64; off <<= 1) {
-    const int u = __shfl_up(v, off), ui = __shfl_up(vi, off);
+    const int u = __shfl_up(v, off), ui = __shfl_up(vi, off), ui2 = __shfl_up(vi2, off);
     if (lane >= off) {
       v += u;
       vi += ui;
+      vi2 += ui2;
     }
   }
   if (lane == 63) {
     wsum[wave] = v;
     wsumi[wave] = vi;
+    wsumi2[wave] = vi2;
   }
   __syncthreads();
-  int base = 0, basei = 0;
+  int base = 0, basei = 0, basei2 = 0;
   for (int w = 0; w < wave; w++) {
     base += wsum[w];
     basei += wsumi[w];
+    basei2 += wsumi2[w];
   }
-  const int excl = base + v - c, excli = basei + vi - ni;
+  const int excl = base + v - c, excli = basei + vi - ni, excli2 = basei2 + vi2 - ni2;
   if (tid < E) {
     counts[tid] = c;
     offsets[tid] = excl;
@@ -127,10 +135,16 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
       const int r = j * BT;
       rec[j] = make_int4(tid, excl + r, c - r < BT ? c - r : BT, 0);
     }
+    int4 *rec2 = items2 ? reinterpret_cast<int4 *>(items2) + 1 + excli2 : nullptr;
+    for (int j = 0; j < ni2; j++) {
+      const int r = j * BT2;
+      rec2[j] = make_int4(tid, excl + r, c - r < BT2 ? c - r : BT2, 0);
+    }
   }
   if (tid == 1023) {  // thread 1023's inclusive sums are the totals
     offsets[E] = base + v;
     tot[0] = basei + vi;
+    tot[1] = basei2 + vi2;
   }
   __syncthreads();
   if (items) {
@@ -140,6 +154,14 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
       reinterpret_cast<int4 *>(items)[1 + tot[0] + j] = make_int4(E, P + r, T - r < BT ? T - r : BT, 1);
     }
     if (tid == 0) items[0] = tot[0] + ns;
+  }
+  if (items2) {
+    const int ns = shared ? (T + BT2 - 1) / BT2 : 0;
+    for (int j = tid; j < ns; j += 1024) {
+      const int r = j * BT2;
+      reinterpret_cast<int4 *>(items2)[1 + tot[1] + j] = make_int4(E, P + r, T - r < BT2 ? T - r : BT2, 1);
+    }
+    if (tid == 0) items2[0] = tot[1] + ns;
   }
   for (int pb = p_lo; pb < p_hi; pb += 64) {
     const int p = pb + lane;

@@ -845,3 +845,129 @@ void k_down_ol(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
       *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
   }
 }
+
+// ---------------------------------------------------------------------------
+// Two octets per wave (items of up to 16 rows): the same weight quad feeds
+// the MFMAs of both octets from registers, so the vector-memory unit carries
+// each weight byte once per 16 tokens instead of once per 8.  The B ring is
+// one quad ahead (2 slots) to leave registers for the second octet.
+template <int NW, int NO, int NG>
+struct oring1 {
+  wq32<NW> w[4];
+  bq32<NO> b[2];
+  uint32_t sc[NG][NW][2];
+};
+
+template <int QL, int NQW, int NW, int NO, int NG, int CPOL>
+__device__ __forceinline__ void o1fixed_from(oring1<NW, NO, NG> &r, const wstream (&ws)[NW], const aoff32 &ao,
+                                             int q0, const gsrc &src, const gsel (&gs)[NO], bool upper, int sb,
+                                             f32x16_t (&acc)[NO][NW]) {
+  if constexpr (QL < NQW) {
+    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG)
+      load_sc32<NW>(r.sc[(QL >> 2) + 1], ws, ao, (q0 >> 2) + (QL >> 2) + 1);
+    if constexpr (QL + 1 < NQW) load_bq32<NO>(r.b[(QL + 1) & 1], src, gs, q0 + QL + 1);
+    if constexpr (QL + 3 < NQW) load_wq32<NW, CPOL>(r.w[(QL + 3) & 3], ws, ao, q0 + QL + 3);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    quad_mma32<QL & 3, NW, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[QL & 1], upper, sb, acc);
+    o1fixed_from<QL + 1, NQW, NW, NO, NG, CPOL>(r, ws, ao, q0, src, gs, upper, sb, acc);
+  }
+}
+
+// K loop over NQW quads from q0 (q0 % 4 == 0) for NO octets, fully unrolled.
+template <int NW, int NO, int CPOL, int NQW>
+__device__ __forceinline__ void o1loop_fixed(const wstream (&ws)[NW], const aoff32 &ao, int q0, const gsrc &src,
+                                             const gsel (&gs)[NO], int lane, f32x16_t (&acc)[NO][NW]) {
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int i = 0; i < NW; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[o][i][e] = 0.0f;
+  constexpr int NG = (NQW + 3) / 4;
+  oring1<NW, NO, NG> r;
+  load_sc32<NW>(r.sc[0], ws, ao, q0 >> 2);
+  load_bq32<NO>(r.b[0], src, gs, q0);
+  load_wq32<NW, CPOL>(r.w[0], ws, ao, q0);
+  if constexpr (NQW > 1) load_wq32<NW, CPOL>(r.w[1], ws, ao, q0 + 1);
+  if constexpr (NQW > 2) load_wq32<NW, CPOL>(r.w[2], ws, ao, q0 + 2);
+  o1fixed_from<0, NQW, NW, NO, NG, CPOL>(r, ws, ao, q0, src, gs, lane_upper32(lane), lane_bscale32(lane), acc);
+}
+
+// k_gate_up_o on items of up to 16 rows: wave w streams unit
+// 2*blockIdx.x + w%2 (gate and up) over K-half w/2 (NQH quads) against one
+// octet (items of <= 8 rows) or two (the same weight registers serve both);
+// the K-halves meet in LDS and each 32-lane half of a wave takes one (unit,
+// token) for clamp + SwiGLU + Q8_0(h), as in k_gate_up_o (same per-octet
+// sums, same bits).  grid (F/64, item capacity), 256 threads.  Requires
+// H == 256*NQH, NQH % 4 == 0.
+template <int NQH>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
+void k_gate_up_o2(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
+                  const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
+                  int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
+                  float *__restrict__ htap) {
+  __shared__ __align__(16) float red[4][2][16][MOE_UNIT];  // [wave][gate/up][token][row]
+  if ((int)blockIdx.y >= items[0]) return;
+  const int4 it = item_of(items, blockIdx.y);
+  const int NQ4 = moe_nq4(2 * NQH), U = F / MOE_UNIT, tiles = F / MOE_TILE, KB = H / MOE_QK;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int ul = wave & 1, kp = wave >> 1, P = T * k;
+  const int u = 2 * blockIdx.x + ul;
+  const int row0 = it.y, nt = it.z;
+  const bool shared = it.w != 0;
+  const int q0 = kp * NQH;
+  const size_t t0 = (size_t)it.x * tiles + 2 * u;
+  const wstream ws[2] = {make_wstream32(w_g, t0, NQ4), make_wstream32(w_u, t0, NQ4)};
+  const aoff32 ao = make_aoff32(lane, NQ4);
+  const gsrc src = make_gsrc(xq, xd, T, KB);
+  gsel gs[2];
+#pragma unroll
+  for (int o = 0; o < 2; o++) {
+    const int i = 8 * o + ((lane & 31) >> 2);
+    int xr = -1;
+    if (i < nt) xr = shared ? row0 + i - P : perm[row0 + i] / k;
+    gs[o] = make_gsel32(lane, xr, KB);
+  }
+  const int n = lane & 31, gb = lane >> 5;
+  if (nt > 8) {
+    f32x16_t acc[2][2];
+    o1loop_fixed<2, 2, 0, NQH>(ws, ao, q0, src, gs, lane, acc);
+#pragma unroll
+    for (int o = 0; o < 2; o++)
+#pragma unroll
+      for (int i = 0; i < 2; i++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const float v = col4_sum(acc[o][i][e]);
+          if ((n & 3) == 0) red[wave][i][8 * o + (n >> 2)][8 * (e >> 2) + 4 * gb + (e & 3)] = v;
+        }
+  } else {
+    const gsel gs1[1] = {gs[0]};
+    f32x16_t acc[1][2];
+    o1loop_fixed<2, 1, 0, NQH>(ws, ao, q0, src, gs1, lane, acc);
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) {
+        const float v = col4_sum(acc[0][i][e]);
+        if ((n & 3) == 0) red[wave][i][n >> 2][8 * (e >> 2) + 4 * gb + (e & 3)] = v;
+      }
+  }
+  __syncthreads();
+  // (unit, token) c = 8*round + 2*wave + half-wave: unit c / 16, token c % 16
+#pragma unroll
+  for (int round = 0; round < 4; round++) {
+    if (8 * (round & 1) >= nt) continue;  // no token of this round is present (uniform over the workgroup)
+    const int c = 8 * round + 2 * wave + (lane >> 5);
+    const int ul2 = c >> 4, t = c & 15, j = lane & 31;
+    const bool live = t < nt;
+    // waves ul2 (K-half 0) and ul2 + 2 (K-half 1) hold this unit
+    const float gsum = red[ul2][0][t][j] + red[ul2 + 2][0][t][j];
+    const float usum = red[ul2][1][t][j] + red[ul2 + 2][1][t][j];
+    const float h = live ? swiglu(gsum, usum, clamp) : 0.0f;
+    const int hrow = row0 + (live ? t : 0), uu = 2 * blockIdx.x + ul2;
+    h_unit_store(h, live, hs + ((size_t)hrow * U + uu) * MOE_XSW, hd + (size_t)hrow * U + uu, lane);
+    if (htap && live) htap[(size_t)hrow * F + (size_t)uu * MOE_UNIT + j] = h;
+  }
+}

@@ -494,7 +494,7 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
     prof_scope ps(c, K_GROUP, (hipStream_t)stream);
     hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, T, 0, 1, counts,
                        offsets, perm, inv, (int32_t *)nullptr, (const float *)nullptr, 0, (uint32_t *)nullptr,
-                       (float *)nullptr);
+                       (float *)nullptr, 0, (int32_t *)nullptr);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
@@ -579,20 +579,34 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   const int BT = oct ? 8 : 4;
   scratch &s = c->sc;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
+  // octets: gate/up on items of up to 16 rows (two octets per wave) where the
+  // shape has an instance and the batch averages 2 pairs per expert or more
+  // (below that most items hold one octet, and k_gate_up_o's deeper B ring
+  // is faster); down keeps items of 8 (a second item list)
+  int32_t *items16 = items + group_list_words(T, k, E);
+  const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 2 == 0 &&
+                  (H == 256 * 28 || H == 256 * 16 || H == 256 * 8);
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
   {
     prof_scope pgr(c, K_GROUP, st);
     hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
-                       shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd);
+                       shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, 16,
+                       o2 ? items16 : (int32_t *)nullptr);
   }
   const int cap = group_item_cap(T, k, E, BT);
   {
     prof_scope pg(c, K_GU_GROUPED, st);
 #define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
-    if (oct) hipLaunchKernelGGL(k_gate_up_o, dim3(F / (2 * MOE_UNIT), cap), dim3(256), 0, st, MOE_GU_ARGS);
+#define MOE_GU_ARGS16 L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items16, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
+    const dim3 g16(F / (2 * MOE_UNIT), group_item_cap(T, k, E, 16));
+    if (o2 && H == 256 * 28) hipLaunchKernelGGL(k_gate_up_o2<28>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    else if (o2 && H == 256 * 16) hipLaunchKernelGGL(k_gate_up_o2<16>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    else if (o2 && H == 256 * 8) hipLaunchKernelGGL(k_gate_up_o2<8>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    else if (oct) hipLaunchKernelGGL(k_gate_up_o, dim3(F / (2 * MOE_UNIT), cap), dim3(256), 0, st, MOE_GU_ARGS);
     else hipLaunchKernelGGL(k_gate_up_g<2>, dim3(F / MOE_UNIT, cap), dim3(256), 0, st, MOE_GU_ARGS);
 #undef MOE_GU_ARGS
+#undef MOE_GU_ARGS16
   }
   s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
   s.last_F = F;

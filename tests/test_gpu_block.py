@@ -214,6 +214,19 @@ def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
     assert_rms_close(ps, refps, what="C1 grouped per-slot")
 
 
+def test_c1_grouped_two_octets_per_wave(blk, torch_dev, oracle, c1):
+    """T = 40 on C1 (160 pairs over 32 experts, >= 2 per expert on average):
+    gate/up runs on items of up to 16 rows with two octets per wave
+    (k_gate_up_o2), down on items of up to 8; items of both sizes occur."""
+    x, lg = wl.make_inputs(c1, 40, 23, zipf=True)
+    ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+    counts = np.bincount(ids.ravel(), minlength=c1.n_expert)
+    say("C1 grouped T=40, pairs per expert", sorted(counts.tolist(), reverse=True)[:8])
+    assert counts.max() > 8 and (counts[counts > 0] <= 8).any()
+    got = run_block(blk, torch_dev, 1, x, ids, wts)
+    check_block(oracle, oracle_layer(oracle, c1, 101, 1, ids), blk, c1, x, ids, wts, got, "C1 grouped T=40")
+
+
 # ---- clamp-active (the reference's synthetic weights never trigger the clamp) ---------
 
 @pytest.mark.parametrize("T", [3, 12])
