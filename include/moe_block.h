@@ -48,7 +48,8 @@ typedef enum {
   MOE_ERR_UNSUPPORTED = -4,   /* shape the kernels do not handle            */
   MOE_ERR_NOT_RESIDENT = -5,  /* layer id has no weights on the device      */
   MOE_ERR_NO_DEVICE = -6,     /* no usable gfx950 device                    */
-  MOE_ERR_INJECTED = -7       /* failure forced by MOE_BLOCK_INJECT         */
+  MOE_ERR_INJECTED = -7,      /* failure forced by MOE_BLOCK_INJECT         */
+  MOE_ERR_FORMAT = -8         /* model file unreadable or not an MXFP4 MoE  */
 } moe_status;
 
 /* Router score functions (glm_dsa/moe_block.h:51-53 sigmoid;
@@ -124,6 +125,48 @@ moe_status moe_layer_generate(moe_ctx *ctx, int layer, const moe_layer_desc *des
  * the shared expert.  For round-trip tests. */
 moe_status moe_layer_read_blocks(moe_ctx *ctx, int layer, int tensor, int expert,
                                  void *out_host);
+
+/* ---- GGUF models --------------------------------------------------------- */
+
+/* One MoE layer of a GGUF model: its shape (H, F, E from the expert
+ * tensors' dims; k = <arch>.expert_used_count; clamp =
+ * <arch>.swiglu_clamp_exp[layer], 0 when absent), and the router settings
+ * the caller passes to moe_route (<arch>.expert_gating_func 1/2/4 ->
+ * MOE_ROUTE_SOFTMAX/SIGMOID/SQRT_SOFTPLUS, -1 when absent or another value;
+ * expert_weights_norm, default 0; expert_weights_scale, default 1).  The
+ * shared expert is part of the layer (desc.has_shared = 1) only when
+ * blk.N.ffn_{gate,up,down}_shexp.weight are MXFP4 of the routed shape and
+ * its clamp (swiglu_clamp_shexp[layer]) equals the routed one; otherwise
+ * the trunk computes it, as in the reference, whose split claims only the
+ * routed experts (moe-serv/src/moe_backend.cpp:289-296). */
+typedef struct {
+  moe_layer_desc desc;
+  int32_t n_layer;     /* <arch>.block_count, -1 when absent            */
+  int32_t route_mode;  /* MOE_ROUTE_*, or -1                            */
+  int32_t route_norm;  /* 0 / 1                                         */
+  float route_scale;   /* multiplier of the routing weights             */
+  int32_t shared_type; /* ggml type of ffn_gate_shexp, -1 when absent   */
+  char arch[32];       /* general.architecture, NUL-terminated          */
+} moe_gguf_layer;
+
+/* Read layer `layer` of the GGUF model at `path` (the first file of a
+ * split model: <stem>-00001-of-000NN.gguf) without a device: the tensors
+ * blk.N.ffn_{gate,up,down}_exps.weight (ggml type 39, MXFP4, dims
+ * [H,F,E], [H,F,E], [F,H,E]) and the keys above.  err (may be NULL)
+ * receives a message on failure: MOE_ERR_INVALID_ARG for a NULL
+ * argument, MOE_ERR_FORMAT for a file that cannot be read, or a layer
+ * without MXFP4 routed experts.  The names are the ones nano-glm binds
+ * (nano-glm/lib/models/deepseek4/model.h:366-372). */
+moe_status moe_gguf_read_layer(const char *path, int layer, moe_gguf_layer *info, char *err,
+                               size_t err_len);
+
+/* Make layer `gguf_layer` of a GGUF model resident as `layer`: the file is
+ * mapped read-only and its expert tensors go through moe_layer_upload.
+ * info (may be NULL) receives what moe_gguf_read_layer reads.  Replaces
+ * the residency step that moe-serv takes from ggml's loaded tensors
+ * (moe_tp_setup_layer, moe_tp.h:551-707, fed by llama.cpp's GGUF loader). */
+moe_status moe_layer_upload_gguf(moe_ctx *ctx, int layer, const char *path, int gguf_layer,
+                                 moe_gguf_layer *info);
 
 /* Free a layer's device memory and return its bytes to the budget
  * (moe_tp_free, moe_tp.h:356-390). */

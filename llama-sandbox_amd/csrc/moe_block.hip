@@ -8,6 +8,7 @@
 #include "../../include/moe_block.h"
 
 #include "device_common.h"
+#include "gguf_reader.h"
 #include "kernels_decode.h"
 #include "kernels_group.h"
 #include "kernels_grouped.h"
@@ -291,6 +292,7 @@ extern "C" const char *moe_status_str(moe_status s) {
     case MOE_ERR_NOT_RESIDENT: return "layer not resident";
     case MOE_ERR_NO_DEVICE: return "no usable gfx950 device";
     case MOE_ERR_INJECTED: return "injected failure";
+    case MOE_ERR_FORMAT: return "model file unreadable or not an MXFP4 MoE layer";
   }
   return "unknown status";
 }
@@ -396,6 +398,107 @@ extern "C" moe_status moe_layer_upload(moe_ctx *c, int layer, const moe_layer_de
   (void)hipFree(stage);
   if (st != MOE_OK) layer_drop(c, layer);
   return st;
+}
+
+// ---- GGUF ------------------------------------------------------------------
+
+// Layer `layer` of an opened model: its shape and router keys into *info,
+// pointers to the six expert tensors' bytes (the shared three NULL when the
+// layer's shared expert is not one this library computes) into w[].
+static moe_status gguf_layer(gguf::model &M, int layer, moe_gguf_layer *info, const uint8_t *w[6]) {
+  memset(info, 0, sizeof(*info));
+  for (int i = 0; i < 6; i++) w[i] = nullptr;
+  std::string arch;
+  if (!M.get_str("general.architecture", &arch) || arch.empty() || arch.size() >= sizeof(info->arch))
+    return M.fail("general.architecture is missing"), MOE_ERR_FORMAT;
+  memcpy(info->arch, arch.data(), arch.size());
+  const std::string a = arch + ".";
+  int64_t v;
+  info->n_layer = M.get_int(a + "block_count", &v) && v >= 0 && v <= INT32_MAX ? (int32_t)v : -1;
+  if (layer < 0 || (info->n_layer >= 0 && layer >= info->n_layer))
+    return M.fail("layer " + std::to_string(layer) + " is out of range"), MOE_ERR_INVALID_ARG;
+  const std::string blk = "blk." + std::to_string(layer) + ".";
+  const char *names[6] = {"ffn_gate_exps.weight", "ffn_up_exps.weight", "ffn_down_exps.weight",
+                          "ffn_gate_shexp.weight", "ffn_up_shexp.weight", "ffn_down_shexp.weight"};
+  const gguf::tensor *t[6];
+  for (int i = 0; i < 6; i++) t[i] = M.find_tensor(blk + names[i]);
+  for (int i = 0; i < 3; i++) {
+    if (!t[i]) return M.fail("no tensor " + blk + names[i]), MOE_ERR_FORMAT;
+    if (t[i]->type != gguf::GGML_TYPE_MXFP4 || t[i]->n_dims != 3)
+      return M.fail(blk + names[i] + ": not a 3-d MXFP4 tensor (type " + std::to_string(t[i]->type) + ")"),
+             MOE_ERR_FORMAT;
+  }
+  const uint64_t H = t[0]->ne[0], F = t[0]->ne[1], E = t[0]->ne[2];
+  if (H == 0 || F == 0 || E == 0 || H % 32 || F % 32 || H > (1u << 20) || F > (1u << 20) || E > (1u << 16) ||
+      t[1]->ne[0] != H || t[1]->ne[1] != F || t[1]->ne[2] != E || t[2]->ne[0] != F || t[2]->ne[1] != H ||
+      t[2]->ne[2] != E)
+    return M.fail(blk + "ffn_*_exps: dims do not form [H,F,E], [H,F,E], [F,H,E] with H, F multiples of 32"),
+           MOE_ERR_FORMAT;
+  if (!M.get_int(a + "expert_used_count", &v) || v < 1 || (uint64_t)v > E)
+    return M.fail(a + "expert_used_count is missing or out of range"), MOE_ERR_FORMAT;
+  const int64_t k = v;
+  if (M.get_int(a + "expert_count", &v) && (uint64_t)v != E)
+    return M.fail(a + "expert_count disagrees with the expert tensors"), MOE_ERR_FORMAT;
+  if (M.get_int(a + "expert_feed_forward_length", &v) && (uint64_t)v != F)
+    return M.fail(a + "expert_feed_forward_length disagrees with the expert tensors"), MOE_ERR_FORMAT;
+  if (M.get_int(a + "embedding_length", &v) && (uint64_t)v != H)
+    return M.fail(a + "embedding_length disagrees with the expert tensors"), MOE_ERR_FORMAT;
+  float clamp = 0.0f;
+  if (M.find(a + "swiglu_clamp_exp") && !M.get_f32_at(a + "swiglu_clamp_exp", (uint64_t)layer, &clamp))
+    return M.fail(a + "swiglu_clamp_exp is not an f32 array covering the layer"), MOE_ERR_FORMAT;
+  for (int i = 0; i < 3; i++)
+    if (!(w[i] = M.data_of(*t[i]))) return MOE_ERR_FORMAT;
+  // the shared expert, when it is one this library computes
+  info->shared_type = t[3] ? (int32_t)t[3]->type : -1;
+  float clamp_sh = 0.0f;
+  const bool sh_clamp_ok = !M.find(a + "swiglu_clamp_shexp") ||
+                           (M.get_f32_at(a + "swiglu_clamp_shexp", (uint64_t)layer, &clamp_sh));
+  bool shared = t[3] && t[4] && t[5] && sh_clamp_ok && clamp_sh == clamp;
+  for (int i = 3; i < 6 && shared; i++) {
+    const uint64_t r0 = i == 5 ? F : H, r1 = i == 5 ? H : F;
+    shared = t[i]->type == gguf::GGML_TYPE_MXFP4 && t[i]->n_dims == 2 && t[i]->ne[0] == r0 && t[i]->ne[1] == r1;
+  }
+  for (int i = 3; i < 6 && shared; i++)
+    if (!(w[i] = M.data_of(*t[i]))) return MOE_ERR_FORMAT;
+  if (!shared) w[3] = w[4] = w[5] = nullptr;
+  info->desc.hidden = (int32_t)H;
+  info->desc.ffn = (int32_t)F;
+  info->desc.n_expert = (int32_t)E;
+  info->desc.n_used = (int32_t)k;
+  info->desc.has_shared = shared ? 1 : 0;
+  info->desc.clamp = clamp;
+  info->route_mode = -1;
+  if (M.get_int(a + "expert_gating_func", &v))
+    info->route_mode = v == 1 ? MOE_ROUTE_SOFTMAX : v == 2 ? MOE_ROUTE_SIGMOID : v == 4 ? MOE_ROUTE_SQRT_SOFTPLUS : -1;
+  info->route_norm = M.get_int(a + "expert_weights_norm", &v) && v != 0 ? 1 : 0;
+  info->route_scale = 1.0f;
+  float sc;
+  if (M.get_f32(a + "expert_weights_scale", &sc)) info->route_scale = sc;
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_gguf_read_layer(const char *path, int layer, moe_gguf_layer *info, char *err,
+                                          size_t err_len) {
+  if (err && err_len) err[0] = 0;
+  if (!path || !info) return MOE_ERR_INVALID_ARG;
+  gguf::model M;
+  const uint8_t *w[6];
+  const moe_status st = M.open(path) ? gguf_layer(M, layer, info, w) : MOE_ERR_FORMAT;
+  if (st != MOE_OK && err && err_len) snprintf(err, err_len, "%s", M.err.c_str());
+  return st;
+}
+
+extern "C" moe_status moe_layer_upload_gguf(moe_ctx *c, int layer, const char *path, int file_layer,
+                                            moe_gguf_layer *info) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!path) return fail(c, MOE_ERR_INVALID_ARG, "moe_layer_upload_gguf: path is NULL");
+  gguf::model M;
+  moe_gguf_layer li;
+  const uint8_t *w[6];
+  const moe_status st = M.open(path) ? gguf_layer(M, file_layer, &li, w) : MOE_ERR_FORMAT;
+  if (st != MOE_OK) return fail(c, st, "moe_layer_upload_gguf: %s", M.err.c_str());
+  if (info) *info = li;
+  return moe_layer_upload(c, layer, &li.desc, w[0], w[1], w[2], w[3], w[4], w[5]);
 }
 
 extern "C" moe_status moe_layer_generate(moe_ctx *c, int layer, const moe_layer_desc *d, uint64_t seed,

@@ -25,6 +25,7 @@ MOE_ERR_UNSUPPORTED = -4
 MOE_ERR_NOT_RESIDENT = -5
 MOE_ERR_NO_DEVICE = -6
 MOE_ERR_INJECTED = -7
+MOE_ERR_FORMAT = -8
 
 MOE_FWD_PER_SLOT = 1
 MOE_FWD_NO_SHARED = 2
@@ -40,6 +41,7 @@ EXPORTS = (
     "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
     "moe_prof_enable", "moe_prof_read", "moe_debug_set_taps",
     "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
+    "moe_gguf_read_layer", "moe_layer_upload_gguf",
 )
 
 
@@ -57,6 +59,13 @@ class LayerDesc(ctypes.Structure):
     def of(cls, shape) -> "LayerDesc":
         return cls(shape.hidden, shape.ffn, shape.n_expert, shape.n_used, int(shape.has_shared),
                    float(shape.clamp))
+
+
+class GgufLayer(ctypes.Structure):
+    """moe_gguf_layer: one MoE layer of a GGUF model (shape and router keys)."""
+    _fields_ = [("desc", LayerDesc), ("n_layer", ctypes.c_int32), ("route_mode", ctypes.c_int32),
+                ("route_norm", ctypes.c_int32), ("route_scale", ctypes.c_float), ("shared_type", ctypes.c_int32),
+                ("arch", ctypes.c_char * 32)]
 
 
 class KernelStat(ctypes.Structure):
@@ -133,9 +142,26 @@ def load_library(path: str | None = None):
     L.moe_debug_wave_sum.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp]
     L.moe_debug_last_h.restype = st
     L.moe_debug_last_h.argtypes = [_vp, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    L.moe_gguf_read_layer.restype = st
+    L.moe_gguf_read_layer.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(GgufLayer), ctypes.c_char_p,
+                                      ctypes.c_size_t]
+    L.moe_layer_upload_gguf.restype = st
+    L.moe_layer_upload_gguf.argtypes = [_vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(GgufLayer)]
     if path is None:
         _lib = L
     return L
+
+
+def read_gguf_layer(path: str, layer: int) -> GgufLayer:
+    """Shape and router keys of one MoE layer of a GGUF model (no device needed);
+    raises MoeError (MOE_ERR_FORMAT for a file that cannot be read as one)."""
+    L = load_library()
+    info = GgufLayer()
+    err = ctypes.create_string_buffer(512)
+    st = L.moe_gguf_read_layer(os.fsencode(path), int(layer), ctypes.byref(info), err, len(err))
+    if st != MOE_OK:
+        raise MoeError(st, f"moe_gguf_read_layer: {err.value.decode(errors='replace')}")
+    return info
 
 
 def _ptr(t) -> int | None:
@@ -221,6 +247,14 @@ class MoeBlock:
         ptrs = [a.ctypes.data if a is not None else None for a in arrs + sh]
         self._check(self.lib.moe_layer_upload(self.h, layer, ctypes.byref(d), *ptrs), "moe_layer_upload")
         self.descs[layer] = d
+
+    def upload_layer_gguf(self, layer: int, path: str, file_layer: int) -> GgufLayer:
+        """Make layer `file_layer` of a GGUF model resident as `layer`."""
+        info = GgufLayer()
+        self._check(self.lib.moe_layer_upload_gguf(self.h, int(layer), os.fsencode(path), int(file_layer),
+                                                   ctypes.byref(info)), "moe_layer_upload_gguf")
+        self.descs[layer] = info.desc
+        return info
 
     def generate_layer(self, layer: int, shape, seed: int, e_lo: int = 124, e_span: int = 7):
         d = LayerDesc.of(shape)

@@ -407,6 +407,48 @@ def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
     g.close()
 
 
+# ---- a layer read from a GGUF model ----------------------------------------------------------
+
+@pytest.mark.parametrize("T", [1, 6])
+def test_layer_from_gguf_model(blk, torch_dev, oracle, tmp_path, T):
+    """A two-layer GGUF model (layer 0 dense, layer 1 MoE with a shared expert
+    and the clamp in swiglu_clamp_exp) written from the generator's blocks:
+    moe_layer_upload_gguf makes layer 1 resident with the file's shape, clamp
+    and router keys, the device holds the file's bytes (read back bit-exact),
+    and the forward matches the oracle on the same blocks."""
+    import gguf_stub as gs
+    shape = wl.LayerShape(hidden=1024, ffn=512, n_expert=16, n_used=4, has_shared=True,
+                          route_mode=wl.ROUTE_SIGMOID, clamp=7.5)
+    H, F, E, k = shape.hidden, shape.ffn, shape.n_expert, shape.n_used
+    seed, lid = 77, 9
+    gen = [np.stack([oracle.gen_mxfp4(seed, lid, t, e, H if t == 2 else F, F if t == 2 else H, 124, 7)
+                     for e in range(E)]) for t in range(3)]
+    sh = tuple(oracle.gen_mxfp4(seed, lid, 3 + t, 0, H if t == 2 else F, F if t == 2 else H, 124, 7)
+               for t in range(3))
+    kvs = gs.moe_keys("deepseek2", 2, H, F, E, k, gating=2, norm=True, scale=1.0, clamp=[0.0, 7.5],
+                      clamp_sh=[0.0, 7.5])
+    tensors = [("blk.0.ffn_gate.weight", [H, 4 * F], gs.F16, bytes(2 * H * 4 * F))]
+    tensors += gs.expert_tensors(1, gen[0], gen[1], gen[2], sh)
+    path = tmp_path / "model.gguf"
+    path.write_bytes(gs.gguf_bytes(kvs, tensors))
+    say("GGUF model", path.stat().st_size, "bytes; T", T)
+    info = blk.upload_layer_gguf(lid, str(path), 1)
+    try:
+        d = info.desc
+        assert (d.hidden, d.ffn, d.n_expert, d.n_used, d.has_shared) == (H, F, E, k, 1)
+        assert d.clamp == np.float32(7.5) and info.route_mode == mb.ROUTE_SIGMOID and info.route_norm == 1
+        for t, e in [(0, 0), (1, 5), (2, E - 1)]:
+            assert np.array_equal(blk.read_blocks(lid, t, e).ravel(), gen[t][e].ravel()), (t, e)
+        assert np.array_equal(blk.read_blocks(lid, 2, E).ravel(), sh[2].ravel())  # shared down
+        x, lg = wl.make_inputs(shape, T, 41)
+        ids, wts = oracle.route(lg, k, info.route_mode, norm=bool(info.route_norm))
+        got = run_block(blk, torch_dev, lid, x, ids, wts)
+        L = oracle_layer(oracle, shape, seed, lid, ids)
+        check_block(oracle, L, blk, shape, x, ids, wts, got, f"GGUF layer T{T}")
+    finally:
+        blk.release_layer(lid)
+
+
 # ---- failure paths, forced from the host ---------------------------------------------------
 
 def test_budget_exhausted_is_reported_not_skipped(torch_dev):
