@@ -168,6 +168,96 @@ moe_status moe_gguf_read_layer(const char *path, int layer, moe_gguf_layer *info
 moe_status moe_layer_upload_gguf(moe_ctx *ctx, int layer, const char *path, int gguf_layer,
                                  moe_gguf_layer *info);
 
+/* ---- nano-glm moe-server protocol v2 ------------------------------------ */
+
+/* The wire format of nano-glm/lib/moe_proto.h:45-157: little-endian, fixed
+ * headers, payload_bytes following each header.  One request is one MoE
+ * layer for one batch: x [n_tokens][n_embd] f32 in, the routed experts'
+ * combined rows [n_tokens][n_embd] f32 out (MOE_RET_COMBINED; the shared
+ * expert stays with the trunk).  A v2 connection starts with a hello. */
+#define MOE_WIRE_MAGIC 0x454F4D4Eu /* "NMOE" */
+#define MOE_WIRE_VERSION 2u
+enum { MOE_WIRE_REQUEST = 1, MOE_WIRE_RESPONSE = 2, MOE_WIRE_HELLO = 3 };
+enum { MOE_WIRE_RET_COMBINED = 0, MOE_WIRE_RET_PER_SLOT = 1 };
+enum {
+  MOE_WIRE_OK = 0,
+  MOE_WIRE_ERR_VERSION = 1,
+  MOE_WIRE_ERR_DIMS = 2,
+  MOE_WIRE_ERR_LAYER = 3,
+  MOE_WIRE_ERR_MODE = 4,
+  MOE_WIRE_ERR_INTERNAL = 5
+};
+
+typedef struct { /* 24 bytes; payload: client fingerprint, key=value lines */
+  uint32_t magic, version, msg_type, reserved;
+  uint64_t payload_bytes;
+} moe_wire_hello_request;
+
+typedef struct { /* 80 bytes; payload: server fingerprint */
+  uint32_t magic, version, msg_type, status;
+  char arch[16];
+  uint32_t n_embd, n_layer, n_dense_lead, n_expert, n_expert_used, n_ff_exp;
+  float expert_scale;
+  uint32_t expert_norm;
+  uint32_t reserved[2];
+  uint64_t payload_bytes;
+} moe_wire_hello_response;
+
+typedef struct { /* 40 bytes; payload: n_embd * n_tokens f32 */
+  uint32_t magic, version, msg_type, layer, n_embd, n_tokens, return_mode, reserved;
+  uint64_t payload_bytes;
+} moe_wire_request;
+
+typedef struct { /* 56 bytes; payload: rows, or an error string if status != 0 */
+  uint32_t magic, version, msg_type, status, n_embd, n_tokens, n_slots, reserved;
+  uint32_t t_parse_us, t_route_us, t_compute_us, t_serialize_us; /* server clock */
+  uint64_t payload_bytes;
+} moe_wire_response;
+
+typedef struct moe_server moe_server;
+
+/* Load a GGUF model's router (blk.N.ffn_gate_inp.weight [H,E] f32/f16/bf16,
+ * blk.N.exp_probs_b.bias [E] when present) and routed experts for every MoE
+ * layer (<arch>.leading_dense_block_count .. block_count - 1) onto `device`
+ * under budget_bytes.  Layers without expert tensors, and deepseek4's
+ * hash-routed layers (<arch>.hash_layer_count), are answered with
+ * MOE_WIRE_ERR_LAYER.  Routing follows the layer's keys (moe_gguf_layer;
+ * no expert_gating_func: sigmoid for glm-dsa, as nano-glm reads it,
+ * glm_dsa/model.h:99-101, softmax otherwise).  Replaces moe-server's model
+ * load (nano-glm/apps/moe-server/main.cpp:331-401).  err (may be NULL)
+ * receives a message on failure. */
+moe_status moe_server_open(const char *gguf_path, int device, uint64_t budget_bytes, moe_server **out,
+                           char *err, size_t err_len);
+void moe_server_close(moe_server *srv);
+const char *moe_server_last_error(const moe_server *srv);
+
+/* One exchange: msg holds one whole message (hello or request header plus
+ * its payload); the whole response (header plus payload) is written to
+ * resp (cap bytes) and its size to *resp_len.  Protocol errors give an
+ * error response (MOE_WIRE_ERR_*, with a message payload) and MOE_OK; a
+ * response that does not fit cap returns MOE_ERR_INVALID_ARG with
+ * *resp_len = the size needed.  The checks and their order follow
+ * serve_hello / serve_one (moe-server/main.cpp:762-880). */
+moe_status moe_server_handle(moe_server *srv, const void *msg, size_t len, void *resp, size_t cap,
+                             size_t *resp_len);
+
+/* TCP (IPv4): bind host:port (port 0 = any free port, returned in
+ * *bound_port), then serve connections one at a time: a hello, then
+ * requests until the peer disconnects or sends a request that gets an
+ * error response (the stream position is then no longer trusted, as in
+ * moe-server).  TCP_NODELAY on every connection (moe_proto.h:206-213).
+ * moe_server_serve returns after max_connections connections (< 0: never).
+ * Replaces moe-server's accept loop (main.cpp:1129-1150). */
+moe_status moe_server_listen(moe_server *srv, const char *host, int port, int *bound_port);
+moe_status moe_server_serve(moe_server *srv, int max_connections);
+
+/* Router logits on the device: logits [T][E] = x [T][H] . W [E][H]^T in f32
+ * (ggml_mul_mat(ffn_gate_inp, x), nano-glm/lib/models/glm_dsa/moe_block.h:52),
+ * H % 4 == 0, pointers 16-byte aligned.  The router of moe_server_*; feeds
+ * moe_route / moe_route_forward. */
+moe_status moe_router_logits(moe_ctx *ctx, const float *w_dev, const float *x_dev, int T, int E, int H,
+                             float *logits_dev, void *stream);
+
 /* Free a layer's device memory and return its bytes to the budget
  * (moe_tp_free, moe_tp.h:356-390). */
 moe_status moe_layer_release(moe_ctx *ctx, int layer);

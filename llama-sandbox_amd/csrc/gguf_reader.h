@@ -32,6 +32,7 @@
 namespace gguf {
 
 enum : uint32_t { T_U8, T_I8, T_U16, T_I16, T_U32, T_I32, T_F32, T_BOOL, T_STR, T_ARR, T_U64, T_I64, T_F64 };
+constexpr uint32_t GGML_TYPE_F32 = 0, GGML_TYPE_F16 = 1, GGML_TYPE_BF16 = 30;
 constexpr uint32_t GGML_TYPE_MXFP4 = 39;  // 32 weights in 17 bytes
 constexpr int MAX_DIMS = 4;
 
@@ -183,10 +184,21 @@ struct model {
   }
 
   // Bytes of a tensor of this type, or 0 when the type is not one this
-  // reader sizes (only MXFP4 tensors are ever read).
+  // reader sizes (MXFP4 experts; f32 / f16 / bf16 router weights and bias).
   static uint64_t bytes_of(const tensor &t) {
-    if (t.type != GGML_TYPE_MXFP4 || t.ne[0] % 32) return 0;
-    uint64_t n = t.ne[0] / 32 * 17;
+    uint64_t n;
+    if (t.type == GGML_TYPE_MXFP4) {
+      if (t.ne[0] % 32) return 0;
+      n = t.ne[0] / 32 * 17;
+    } else if (t.type == GGML_TYPE_F32) {
+      if (t.ne[0] > UINT64_MAX / 4) return 0;
+      n = t.ne[0] * 4;
+    } else if (t.type == GGML_TYPE_F16 || t.type == GGML_TYPE_BF16) {
+      if (t.ne[0] > UINT64_MAX / 2) return 0;
+      n = t.ne[0] * 2;
+    } else {
+      return 0;
+    }
     for (int d = 1; d < MAX_DIMS; d++) {
       if (t.ne[d] && n > UINT64_MAX / t.ne[d]) return 0;
       n *= t.ne[d];
@@ -198,10 +210,56 @@ struct model {
   const uint8_t *data_of(const tensor &t) {
     const mapped &f = *files[t.shard];
     const uint64_t n = bytes_of(t);
-    if (n == 0) return fail("tensor " + t.name + " is not an MXFP4 tensor of whole blocks"), nullptr;
+    if (n == 0) return fail("tensor " + t.name + " has a type or shape this reader does not size"), nullptr;
     if (t.rel > f.n || f.data > f.n - t.rel || n > f.n - f.data - t.rel)
       return fail("tensor " + t.name + " runs past the end of its file"), nullptr;
     return f.p + f.data + t.rel;
+  }
+
+  // An f32 / f16 / bf16 tensor of `count` elements as f32 into out.
+  bool read_f32(const tensor &t, uint64_t count, std::vector<float> &out) {
+    uint64_t ne = 1;
+    for (int d = 0; d < MAX_DIMS && ne <= count; d++) ne = t.ne[d] <= count ? ne * t.ne[d] : count + 1;
+    if (ne != count) return fail("tensor " + t.name + " does not hold " + std::to_string(count) + " elements");
+    if (t.type != GGML_TYPE_F32 && t.type != GGML_TYPE_F16 && t.type != GGML_TYPE_BF16)
+      return fail("tensor " + t.name + " is not f32, f16 or bf16 (type " + std::to_string(t.type) + ")");
+    const uint8_t *p = data_of(t);
+    if (!p) return false;
+    out.resize(count);
+    for (uint64_t i = 0; i < count; i++) {
+      if (t.type == GGML_TYPE_F32) {
+        memcpy(&out[i], p + 4 * i, 4);
+      } else {
+        uint16_t h;
+        memcpy(&h, p + 2 * i, 2);
+        out[i] = t.type == GGML_TYPE_BF16 ? bf16_to_f32(h) : f16_to_f32(h);
+      }
+    }
+    return true;
+  }
+
+  static float bf16_to_f32(uint16_t h) {
+    const uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+  }
+  // IEEE binary16 -> binary32, exact (subnormals, inf and NaN included).
+  static float f16_to_f32(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h >> 15) << 31, ex = (h >> 10) & 31, man = h & 1023;
+    uint32_t u;
+    if (ex == 31) {
+      u = sign | 0x7f800000u | (man << 13);
+    } else if (ex) {
+      u = sign | ((ex + 112) << 23) | (man << 13);
+    } else {
+      float f = (float)man * 0x1p-24f;  // subnormal or zero: exact in f32
+      memcpy(&u, &f, 4);
+      u |= sign;
+    }
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
   }
 
   bool open_one(const std::string &path, bool first) {

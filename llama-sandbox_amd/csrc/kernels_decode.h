@@ -107,6 +107,36 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 }
 
 // ---------------------------------------------------------------------------
+// Router logits for the moe-server protocol: logits[t][e] = sum_h W[e][h] *
+// x[t][h] in f32 (ggml_mul_mat of ffn_gate_inp [H, E] with x [H, T],
+// nano-glm/lib/models/glm_dsa/moe_block.h:52).  One wave per expert and 4
+// tokens: each lane accumulates a strided quarter-row slice with FMAs, then
+// wave_sum.  grid (ceil(E/4), ceil(T/4)), 256 threads; H % 4 == 0, rows
+// 16-byte aligned.
+__global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__ W, const float *__restrict__ x,
+                                                       int T, int E, int H, float *__restrict__ logits) {
+  const int lane = threadIdx.x & 63;
+  const int e = blockIdx.x * 4 + (threadIdx.x >> 6), t0 = blockIdx.y * 4;
+  if (e >= E) return;  // whole waves
+  const float4 *w4 = reinterpret_cast<const float4 *>(W + (size_t)e * H);
+  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int i = lane; i < H / 4; i += 64) {
+    const float4 w = w4[i];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      if (t0 + j >= T) break;
+      const float4 v = reinterpret_cast<const float4 *>(x + (size_t)(t0 + j) * H)[i];
+      acc[j] = fmaf(w.x, v.x, fmaf(w.y, v.y, fmaf(w.z, v.z, fmaf(w.w, v.w, acc[j]))));
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const float v = wave_sum(acc[j]);
+    if (lane == 0 && t0 + j < T) logits[(size_t)(t0 + j) * E + e] = v;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // test hook: one wave_sum per 64 inputs
 __global__ __launch_bounds__(64) void k_debug_wave_sum(const float *__restrict__ x,
                                                        float *__restrict__ out) {

@@ -586,6 +586,18 @@ extern "C" moe_status moe_route(moe_ctx *c, const float *logits, const float *bi
   return MOE_OK;
 }
 
+extern "C" moe_status moe_router_logits(moe_ctx *c, const float *w, const float *x, int T, int E, int H,
+                                        float *logits, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (!w || !x || !logits || T <= 0 || E <= 0 || H <= 0 || H % 4 || ((uintptr_t)w | (uintptr_t)x) % 16)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_router_logits: bad arguments");
+  HIPC(c, hipSetDevice(c->device));
+  hipLaunchKernelGGL(k_router_logits, dim3(ceil_div(E, 4), ceil_div(T, 4)), dim3(256), 0, (hipStream_t)stream, w, x,
+                     T, E, H, logits);
+  HIPC(c, hipGetLastError());
+  return MOE_OK;
+}
+
 extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, int E, int32_t *counts,
                                 int32_t *offsets, int32_t *perm, int32_t *inv, void *stream) {
   if (!c) return MOE_ERR_INVALID_ARG;
@@ -938,3 +950,5 @@ extern "C" moe_status moe_debug_last_h(moe_ctx *c, float *h, size_t cap, size_t 
   *n = cnt;
   return MOE_OK;
 }
+
+#include "moe_server.h"

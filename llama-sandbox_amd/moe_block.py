@@ -42,7 +42,15 @@ EXPORTS = (
     "moe_prof_enable", "moe_prof_read", "moe_debug_set_taps",
     "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
     "moe_gguf_read_layer", "moe_layer_upload_gguf",
+    "moe_server_open", "moe_server_close", "moe_server_last_error", "moe_server_handle", "moe_server_listen",
+    "moe_server_serve", "moe_router_logits",
 )
+
+# nano-glm moe-server protocol v2 (include/moe_block.h, moe_wire_*)
+WIRE_MAGIC, WIRE_VERSION = 0x454F4D4E, 2
+WIRE_REQUEST, WIRE_RESPONSE, WIRE_HELLO = 1, 2, 3
+WIRE_RET_COMBINED, WIRE_RET_PER_SLOT = 0, 1
+WIRE_OK, WIRE_ERR_VERSION, WIRE_ERR_DIMS, WIRE_ERR_LAYER, WIRE_ERR_MODE, WIRE_ERR_INTERNAL = range(6)
 
 
 class MoeError(RuntimeError):
@@ -66,6 +74,31 @@ class GgufLayer(ctypes.Structure):
     _fields_ = [("desc", LayerDesc), ("n_layer", ctypes.c_int32), ("route_mode", ctypes.c_int32),
                 ("route_norm", ctypes.c_int32), ("route_scale", ctypes.c_float), ("shared_type", ctypes.c_int32),
                 ("arch", ctypes.c_char * 32)]
+
+
+class WireHelloRequest(ctypes.Structure):
+    _fields_ = [("magic", ctypes.c_uint32), ("version", ctypes.c_uint32), ("msg_type", ctypes.c_uint32),
+                ("reserved", ctypes.c_uint32), ("payload_bytes", ctypes.c_uint64)]
+
+
+class WireHelloResponse(ctypes.Structure):
+    _fields_ = [("magic", ctypes.c_uint32), ("version", ctypes.c_uint32), ("msg_type", ctypes.c_uint32),
+                ("status", ctypes.c_uint32), ("arch", ctypes.c_char * 16), ("n_embd", ctypes.c_uint32),
+                ("n_layer", ctypes.c_uint32), ("n_dense_lead", ctypes.c_uint32), ("n_expert", ctypes.c_uint32),
+                ("n_expert_used", ctypes.c_uint32), ("n_ff_exp", ctypes.c_uint32), ("expert_scale", ctypes.c_float),
+                ("expert_norm", ctypes.c_uint32), ("reserved", ctypes.c_uint32 * 2),
+                ("payload_bytes", ctypes.c_uint64)]
+
+
+class WireRequest(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("magic", "version", "msg_type", "layer", "n_embd", "n_tokens",
+                                               "return_mode", "reserved")] + [("payload_bytes", ctypes.c_uint64)]
+
+
+class WireResponse(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_uint32) for n in ("magic", "version", "msg_type", "status", "n_embd", "n_tokens",
+                                               "n_slots", "reserved", "t_parse_us", "t_route_us", "t_compute_us",
+                                               "t_serialize_us")] + [("payload_bytes", ctypes.c_uint64)]
 
 
 class KernelStat(ctypes.Structure):
@@ -147,6 +180,21 @@ def load_library(path: str | None = None):
                                       ctypes.c_size_t]
     L.moe_layer_upload_gguf.restype = st
     L.moe_layer_upload_gguf.argtypes = [_vp, ctypes.c_int, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(GgufLayer)]
+    L.moe_server_open.restype = st
+    L.moe_server_open.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.c_uint64, ctypes.POINTER(_vp),
+                                  ctypes.c_char_p, ctypes.c_size_t]
+    L.moe_server_close.restype = None
+    L.moe_server_close.argtypes = [_vp]
+    L.moe_server_last_error.restype = ctypes.c_char_p
+    L.moe_server_last_error.argtypes = [_vp]
+    L.moe_server_handle.restype = st
+    L.moe_server_handle.argtypes = [_vp, _vp, ctypes.c_size_t, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    L.moe_server_listen.restype = st
+    L.moe_server_listen.argtypes = [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
+    L.moe_server_serve.restype = st
+    L.moe_server_serve.argtypes = [_vp, ctypes.c_int]
+    L.moe_router_logits.restype = st
+    L.moe_router_logits.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]
     if path is None:
         _lib = L
     return L
@@ -285,6 +333,13 @@ class MoeBlock:
         self._check(self.lib.moe_route(self.h, _ptr(logits), _ptr(bias), T, E, k, mode, int(norm), scale,
                                        _ptr(ids), _ptr(wts), _stream(stream)), "moe_route")
 
+    def router_logits(self, w, x, logits, stream=None):
+        """logits [T][E] = x [T][H] . w [E][H]^T (f32 device tensors)."""
+        T, H = x.shape
+        E = w.shape[0]
+        self._check(self.lib.moe_router_logits(self.h, _ptr(w), _ptr(x), T, E, H, _ptr(logits), _stream(stream)),
+                    "moe_router_logits")
+
     def group(self, ids, E: int, counts, offsets, perm, inv=None, stream=None):
         T, k = ids.shape
         self._check(self.lib.moe_group(self.h, _ptr(ids), T, k, E, _ptr(counts), _ptr(offsets), _ptr(perm),
@@ -354,3 +409,65 @@ class MoeBlock:
         n = ctypes.c_size_t()
         self._check(self.lib.moe_debug_last_h(self.h, buf.ctypes.data, cap, ctypes.byref(n)), "moe_debug_last_h")
         return buf[: n.value]
+
+
+class MoeServer:
+    """nano-glm moe-server protocol v2 served from the MoE block
+    (moe_server_open / handle / listen / serve)."""
+
+    def __init__(self, gguf_path: str, device: int = 0, budget_bytes: int = 2 ** 64 - 1,
+                 lib_path: str | None = None):
+        self.lib = load_library(lib_path)
+        h = _vp()
+        err = ctypes.create_string_buffer(512)
+        st = self.lib.moe_server_open(os.fsencode(gguf_path), device, budget_bytes, ctypes.byref(h), err, len(err))
+        if st != MOE_OK:
+            raise MoeError(st, f"moe_server_open: {self.lib.moe_status_str(st).decode()}: "
+                               f"{err.value.decode(errors='replace')}")
+        self.h = h.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.lib.moe_server_close(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *a):
+        self.close()
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def _check(self, st: int, what: str):
+        if st != MOE_OK:
+            msg = self.lib.moe_server_last_error(self.h).decode() if self.h else ""
+            raise MoeError(st, f"{what}: {self.lib.moe_status_str(st).decode()}: {msg}")
+
+    def handle(self, msg: bytes) -> bytes:
+        """One whole message in, the whole response out."""
+        n = ctypes.c_size_t()
+        cap = 1 << 16
+        while True:
+            buf = ctypes.create_string_buffer(cap)
+            st = self.lib.moe_server_handle(self.h, msg, len(msg), buf, cap, ctypes.byref(n))
+            if st == MOE_OK:
+                return buf.raw[: n.value]
+            if st == MOE_ERR_INVALID_ARG and n.value > cap:
+                cap = n.value
+                continue
+            self._check(st, "moe_server_handle")
+
+    def listen(self, host: str = "127.0.0.1", port: int = 0) -> int:
+        """Bind; returns the port (port 0 = any free one)."""
+        bound = ctypes.c_int()
+        self._check(self.lib.moe_server_listen(self.h, host.encode(), port, ctypes.byref(bound)), "moe_server_listen")
+        return bound.value
+
+    def serve(self, max_connections: int = -1):
+        """Serve connections one at a time (blocks; ctypes releases the GIL)."""
+        self._check(self.lib.moe_server_serve(self.h, max_connections), "moe_server_serve")

@@ -13,7 +13,8 @@ import numpy as np
 U8, I8, U16, I16, U32, I32, F32, BOOL, STR, ARR, U64, I64, F64 = range(13)
 _FMT = {U8: "<B", I8: "<b", U16: "<H", I16: "<h", U32: "<I", I32: "<i", F32: "<f", BOOL: "<?",
         U64: "<Q", I64: "<q", F64: "<d"}
-F16, Q8_0, MXFP4 = 1, 8, 39
+# ggml tensor types (not the key/value types above)
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16, GGML_MXFP4 = 0, 1, 8, 30, 39
 
 
 def _str(s) -> bytes:
@@ -70,15 +71,15 @@ def moe_keys(arch: str, n_layer: int, H: int, F: int, E: int, k: int, gating=2, 
 
 
 def expert_tensors(layer: int, gate: np.ndarray, up: np.ndarray, down: np.ndarray, shared=None,
-                   shared_type: int = MXFP4):
+                   shared_type: int = GGML_MXFP4):
     """gate/up uint8 [E, F, H/32, 17], down [E, H, F/32, 17]; shared (gate, up,
     down) [F, H/32, 17], [F, H/32, 17], [H, F/32, 17] or None."""
     E, F, kbh, _ = gate.shape
     H = kbh * 32
     b = f"blk.{layer}."
-    t = [(b + "ffn_gate_exps.weight", [H, F, E], MXFP4, gate.tobytes()),
-         (b + "ffn_up_exps.weight", [H, F, E], MXFP4, up.tobytes()),
-         (b + "ffn_down_exps.weight", [F, H, E], MXFP4, down.tobytes())]
+    t = [(b + "ffn_gate_exps.weight", [H, F, E], GGML_MXFP4, gate.tobytes()),
+         (b + "ffn_up_exps.weight", [H, F, E], GGML_MXFP4, up.tobytes()),
+         (b + "ffn_down_exps.weight", [F, H, E], GGML_MXFP4, down.tobytes())]
     if shared is not None:
         sg, su, sd = shared
         t += [(b + "ffn_gate_shexp.weight", [H, F], shared_type, sg.tobytes()),

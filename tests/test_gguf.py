@@ -30,14 +30,14 @@ def write(tmp_path, kvs, tensors, name="m.gguf", **kw):
     return str(p)
 
 
-def model(tmp_path, arch="deepseek2", clamp=None, clamp_sh=None, shared=True, shared_type=gs.MXFP4, gating=2,
+def model(tmp_path, arch="deepseek2", clamp=None, clamp_sh=None, shared=True, shared_type=gs.GGML_MXFP4, gating=2,
           **kw):
     """Two layers: 0 dense (no expert tensors), 1 MoE."""
     g, u, d, sh = layer_arrays(shared=shared)
-    if sh is not None and shared_type != gs.MXFP4:
+    if sh is not None and shared_type != gs.GGML_MXFP4:
         sh = tuple(np.zeros(a.size, np.uint8) for a in sh)  # stand-in bytes of another type
     kvs = gs.moe_keys(arch, 2, H, F, E, K, gating=gating, clamp=clamp, clamp_sh=clamp_sh)
-    tensors = [("blk.0.ffn_gate.weight", [H, F], gs.F16, bytes(2 * H * F))]
+    tensors = [("blk.0.ffn_gate.weight", [H, F], gs.GGML_F16, bytes(2 * H * F))]
     tensors += gs.expert_tensors(1, g, u, d, sh, shared_type)
     return write(tmp_path, kvs, tensors, **kw)
 
@@ -59,7 +59,7 @@ def test_layer_shape_and_router_keys(tmp_path):
     assert d.clamp == 7.5
     assert info.arch == b"deepseek2" and info.n_layer == 2
     assert (info.route_mode, info.route_norm, info.route_scale) == (mb.ROUTE_SIGMOID, 1, 2.5)
-    assert info.shared_type == gs.MXFP4
+    assert info.shared_type == gs.GGML_MXFP4
 
 
 @pytest.mark.parametrize("gating, mode", [(1, mb.ROUTE_SOFTMAX), (2, mb.ROUTE_SIGMOID),
@@ -74,12 +74,12 @@ def test_no_clamp_key_means_no_clamp(tmp_path):
 
 def test_shared_expert_with_another_clamp_is_left_to_the_trunk(tmp_path):
     info = read(model(tmp_path, clamp=[0.0, 7.5], clamp_sh=[0.0, 10.0]))
-    assert info.desc.has_shared == 0 and info.shared_type == gs.MXFP4
+    assert info.desc.has_shared == 0 and info.shared_type == gs.GGML_MXFP4
 
 
 def test_shared_expert_of_another_type_is_left_to_the_trunk(tmp_path):
-    info = read(model(tmp_path, shared_type=gs.Q8_0))
-    assert info.desc.has_shared == 0 and info.shared_type == gs.Q8_0
+    info = read(model(tmp_path, shared_type=gs.GGML_Q8_0))
+    assert info.desc.has_shared == 0 and info.shared_type == gs.GGML_Q8_0
 
 
 def test_no_shared_expert(tmp_path):
@@ -106,7 +106,7 @@ def test_split_model(tmp_path):
     """Metadata in the first file, the layer's tensors in the second."""
     g, u, d, sh = layer_arrays()
     kvs = gs.moe_keys("deepseek2", 2, H, F, E, K)
-    write(tmp_path, kvs, [("blk.0.ffn_gate.weight", [H, F], gs.F16, bytes(2 * H * F))],
+    write(tmp_path, kvs, [("blk.0.ffn_gate.weight", [H, F], gs.GGML_F16, bytes(2 * H * F))],
           name="m-00001-of-00002.gguf")
     first = str(tmp_path / "m-00001-of-00002.gguf")
     st, msg = status_of(first)
@@ -130,11 +130,11 @@ def test_malformed_files(tmp_path, case):
         kvs = [x for x in kvs if x[0] != key] + ([(key, t, v)] if t is not None else [])
 
     if case == "routed_type":
-        tensors[0] = (tensors[0][0], tensors[0][1], gs.Q8_0, tensors[0][3])
+        tensors[0] = (tensors[0][0], tensors[0][1], gs.GGML_Q8_0, tensors[0][3])
     elif case == "dims":
-        tensors[2] = (tensors[2][0], [H, F, E], gs.MXFP4, tensors[2][3])
+        tensors[2] = (tensors[2][0], [H, F, E], gs.GGML_MXFP4, tensors[2][3])
     elif case == "ndims":
-        tensors[1] = (tensors[1][0], [H, F * E], gs.MXFP4, tensors[1][3])
+        tensors[1] = (tensors[1][0], [H, F * E], gs.GGML_MXFP4, tensors[1][3])
     elif case == "used_missing":
         set_key("deepseek2.expert_used_count", None, None)
     elif case == "used_range":
@@ -156,7 +156,7 @@ def test_malformed_files(tmp_path, case):
         set_key("x.nested", gs.ARR, (gs.ARR, []))
     elif case == "misaligned":
         kvs.append(("general.alignment", gs.U32, 64))  # tensors laid out at 32: the second starts at 32
-        tensors.insert(0, ("blk.0.attn_norm.weight", [8], 0, bytes(32)))
+        tensors.insert(0, ("blk.0.attn_norm.weight", [8], gs.GGML_F32, bytes(32)))
     raw = bytearray(gs.gguf_bytes(kvs, tensors, **kw))
     if case == "magic":
         raw[0:4] = b"GGML"

@@ -427,7 +427,7 @@ def test_layer_from_gguf_model(blk, torch_dev, oracle, tmp_path, T):
                for t in range(3))
     kvs = gs.moe_keys("deepseek2", 2, H, F, E, k, gating=2, norm=True, scale=1.0, clamp=[0.0, 7.5],
                       clamp_sh=[0.0, 7.5])
-    tensors = [("blk.0.ffn_gate.weight", [H, 4 * F], gs.F16, bytes(2 * H * 4 * F))]
+    tensors = [("blk.0.ffn_gate.weight", [H, 4 * F], gs.GGML_F16, bytes(2 * H * 4 * F))]
     tensors += gs.expert_tensors(1, gen[0], gen[1], gen[2], sh)
     path = tmp_path / "model.gguf"
     path.write_bytes(gs.gguf_bytes(kvs, tensors))
