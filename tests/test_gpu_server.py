@@ -217,3 +217,54 @@ def test_tcp_connections(server, model):
             except OSError:
                 pass
             th.join(timeout=10)
+
+
+def test_deepseek4_model(tmp_path, oracle, torch_dev):
+    """deepseek4 keys: sqrt-softplus gating (expert_gating_func 4), a per-layer
+    SwiGLU clamp (swiglu_clamp_exp), hash-routed leading layers
+    (hash_layer_count: answered with a LAYER error) and no dense lead."""
+    torch, dev = torch_dev
+    rng = np.random.default_rng(7)
+    kvs = gs.moe_keys("deepseek4", 3, H, F, E, K, gating=4, norm=True, scale=1.5, clamp=[7.0, 7.0, 7.0],
+                      clamp_sh=[7.0, 7.0, 7.0])
+    kvs.append(("deepseek4.hash_layer_count", gs.U32, 2))
+    tensors = []
+    for il in (1, 2):
+        g = [np.stack([oracle.gen_mxfp4(SEED, 10 + il, t, e, H if t == 2 else F, F if t == 2 else H)
+                       for e in range(E)]) for t in range(3)]
+        sh = tuple(oracle.gen_mxfp4(SEED, 10 + il, 3 + t, 0, H if t == 2 else F, F if t == 2 else H) for t in range(3))
+        tensors += gs.expert_tensors(il, g[0], g[1], g[2], sh)
+        w = (rng.standard_normal((E, H)) * 0.05).astype(np.float32)
+        tensors.append((f"blk.{il}.ffn_gate_inp.weight", [H, E], gs.GGML_F32, w.tobytes()))
+    path = tmp_path / "ds4.gguf"
+    path.write_bytes(gs.gguf_bytes(kvs, tensors))
+    srv = mb.MoeServer(str(path), 0)
+    blk = mb.MoeBlock(0)
+    try:
+        hq = mb.WireHelloRequest(mb.WIRE_MAGIC, mb.WIRE_VERSION, mb.WIRE_HELLO, 0, 0)
+        h = mb.WireHelloResponse.from_buffer_copy(srv.handle(bytes(hq))[:80])
+        assert (h.arch, h.n_layer, h.n_dense_lead, h.expert_scale) == (b"deepseek4", 3, 0, 1.5)
+        x, _ = wl.make_inputs(SHAPE, 4, 77)
+        for layer in (0, 1):
+            rh, body = parse_response(srv.handle(request(layer, x)))
+            assert rh.status == mb.WIRE_ERR_LAYER, (layer, body)
+        rh, body = parse_response(srv.handle(request(2, x)))
+        assert rh.status == mb.WIRE_OK, body[:200]
+        info = blk.upload_layer_gguf(202, str(path), 2)
+        assert info.desc.clamp == 7.0 and info.route_mode == mb.ROUTE_SQRT_SOFTPLUS and info.desc.has_shared == 1
+        w = np.frombuffer(tensors[-1][3], np.float32).reshape(E, H)
+        xd = torch.from_numpy(x).to(dev)
+        lg = torch.empty((4, E), dtype=torch.float32, device=dev)
+        blk.router_logits(torch.from_numpy(w.copy()).to(dev), xd, lg)
+        ids = torch.empty((4, K), dtype=torch.int32, device=dev)
+        wts = torch.empty((4, K), dtype=torch.float32, device=dev)
+        out = torch.empty((4, H), dtype=torch.float32, device=dev)
+        blk.route_forward(202, xd, lg, ids, wts, out, mb.ROUTE_SQRT_SOFTPLUS, norm=True, scale=1.5,
+                          flags=mb.MOE_FWD_NO_SHARED)
+        torch.cuda.synchronize()
+        ref = out.cpu().numpy()
+        got = np.frombuffer(body, np.float32).reshape(4, H)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    finally:
+        blk.close()
+        srv.close()
