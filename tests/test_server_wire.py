@@ -25,3 +25,20 @@ def test_server_open_without_a_device(tmp_path):
     with pytest.raises(mb.MoeError) as ei:
         mb.MoeServer(str(tmp_path / "absent.gguf"))
     assert ei.value.status == mb.MOE_ERR_NO_DEVICE
+
+
+def test_moe_server_binary_usage_and_no_device(tmp_path):
+    """The C++ moe-server: usage on bad arguments (exit 2); on a host without
+    a gfx950 device, a clear error (exit 1)."""
+    import os
+    import subprocess
+    exe = os.path.join(os.path.dirname(mb.LIB_PATH), "moe-server")
+    assert os.path.exists(exe), "moe-server is built with the library"
+    r = subprocess.run([exe], capture_output=True, text=True, timeout=60)
+    assert r.returncode == 2 and "Usage: moe-server -m" in r.stderr
+    import torch
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    r = subprocess.run([exe, "-m", str(tmp_path / "absent.gguf"), "--port", "0"], capture_output=True, text=True,
+                       timeout=60)
+    assert r.returncode == 1 and "no usable gfx950 device" in r.stderr
