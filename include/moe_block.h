@@ -168,6 +168,81 @@ moe_status moe_gguf_read_layer(const char *path, int layer, moe_gguf_layer *info
 moe_status moe_layer_upload_gguf(moe_ctx *ctx, int layer, const char *path, int gguf_layer,
                                  moe_gguf_layer *info);
 
+/* ---- the ggml backend's claim set and split, without ggml ---------------- */
+
+/* One graph node as the ggml backend sees it, filled from a ggml_tensor
+ * field for field by the adapter (which has ggml's headers; this library
+ * does not).  op: MOE_NODE_*; type: ggml's type number (0 f32, 26 i32,
+ * 39 mxfp4); glu_op / glu_swapped: a GLU node's op_params[0] / [1]
+ * (ggml's glu op numbering, SwiGLU = 2); clamp_min / clamp_max: a CLAMP
+ * node's op_params as floats; in_moe_buffer: the storage of the node (of
+ * its view_src when it is a view) is the MoE buffer type. */
+enum {
+  MOE_NODE_NONE = 0,
+  MOE_NODE_RESHAPE,
+  MOE_NODE_VIEW,
+  MOE_NODE_PERMUTE,
+  MOE_NODE_TRANSPOSE,
+  MOE_NODE_MUL_MAT_ID,
+  MOE_NODE_CLAMP,
+  MOE_NODE_MUL,
+  MOE_NODE_GLU,
+  MOE_NODE_ADD,
+  MOE_NODE_OTHER
+};
+#define MOE_GLU_SWIGLU 2
+#define MOE_GGML_F32 0
+#define MOE_GGML_I32 26
+#define MOE_GGML_MXFP4 39
+
+typedef struct moe_node {
+  int32_t op, type;
+  int64_t ne[4];
+  int32_t contiguous;
+  int32_t in_moe_buffer;
+  int32_t glu_op, glu_swapped;
+  float clamp_min, clamp_max;
+  const struct moe_node *src[3];
+  const struct moe_node *view_src;
+  void *data;
+  const char *name;
+} moe_node;
+
+/* Does the backend claim this node?  Views and reshapes: yes (free);
+ * MUL_MAT_ID: iff its weights (src[0]) are in the MoE buffer; CLAMP and
+ * MUL: iff they descend within 4 links from such a MUL_MAT_ID; GLU: iff
+ * SwiGLU and so descended; ADD and everything else: no (ADD is also the
+ * trunk's residual add).  MOESERV_DISABLE set in the environment: claim
+ * nothing.  Restates moeserv_device_supports_op / moeserv_is_ours /
+ * moeserv_derives_from_ours (moe-serv/src/moe_backend.cpp:262-345). */
+int moe_node_claimed(const moe_node *node);
+
+/* The routed-expert split of one MoE layer, parsed from the nodes the
+ * backend received: the MUL node (the router-weight multiply) whose src[0]
+ * is the down MUL_MAT_ID, whose input is the GLU (SwiGLU, not swapped) of
+ * the gate and up MUL_MAT_IDs, each optionally through a CLAMP; shared x
+ * and ids; f32 x / wts / out, i32 ids, MXFP4 weights; the layer id from
+ * the gate weight's name "blk.N.".  Clamps: gate [gate_min, gate_max], up
+ * [up_min, up_max] (infinite when absent).  Restates moe_tp_parse
+ * (moe-serv/src/moe_tp.h:301-354), with more than one token allowed. */
+typedef struct {
+  const moe_node *gate_w, *up_w, *down_w, *x, *ids, *wts, *out;
+  float gate_min, gate_max, up_min, up_max;
+  int32_t layer, n_slots, n_tokens, hidden, ffn, n_expert;
+} moe_split;
+
+/* MOE_OK, or MOE_ERR_UNSUPPORTED with the reason in why (may be NULL). */
+moe_status moe_split_parse(const moe_node *const *nodes, int n_nodes, moe_split *split, char *why,
+                           size_t why_len);
+
+/* Compute a split on the device: parse, check it against resident layer
+ * split.layer (shape; clamps of the form gate <= L, up in [-L, L] with the
+ * layer's L), then moe_forward_host with MOE_FWD_PER_SLOT into out's host
+ * data ([T][k][H], the MUL node).  Any failure is a status other than
+ * MOE_OK and the caller runs the split on its CPU path, never skips it
+ * (moeserv_backend_graph_compute, moe_backend.cpp:413-484). */
+moe_status moe_split_compute(moe_ctx *ctx, const moe_node *const *nodes, int n_nodes);
+
 /* ---- nano-glm moe-server protocol v2 ------------------------------------ */
 
 /* The wire format of nano-glm/lib/moe_proto.h:45-157: little-endian, fixed

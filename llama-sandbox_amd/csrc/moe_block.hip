@@ -952,3 +952,4 @@ extern "C" moe_status moe_debug_last_h(moe_ctx *c, float *h, size_t cap, size_t 
 }
 
 #include "moe_server.h"
+#include "graph_split.h"

@@ -43,8 +43,14 @@ EXPORTS = (
     "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
     "moe_gguf_read_layer", "moe_layer_upload_gguf",
     "moe_server_open", "moe_server_close", "moe_server_last_error", "moe_server_handle", "moe_server_listen",
-    "moe_server_serve", "moe_router_logits",
+    "moe_server_serve", "moe_router_logits", "moe_node_claimed", "moe_split_parse", "moe_split_compute",
 )
+
+# graph nodes of the ggml backend's split (include/moe_block.h, moe_node)
+(NODE_NONE, NODE_RESHAPE, NODE_VIEW, NODE_PERMUTE, NODE_TRANSPOSE, NODE_MUL_MAT_ID, NODE_CLAMP, NODE_MUL, NODE_GLU,
+ NODE_ADD, NODE_OTHER) = range(11)
+GLU_SWIGLU = 2
+GGML_F32, GGML_I32, GGML_MXFP4 = 0, 26, 39
 
 # nano-glm moe-server protocol v2 (include/moe_block.h, moe_wire_*)
 WIRE_MAGIC, WIRE_VERSION = 0x454F4D4E, 2
@@ -99,6 +105,23 @@ class WireResponse(ctypes.Structure):
     _fields_ = [(n, ctypes.c_uint32) for n in ("magic", "version", "msg_type", "status", "n_embd", "n_tokens",
                                                "n_slots", "reserved", "t_parse_us", "t_route_us", "t_compute_us",
                                                "t_serialize_us")] + [("payload_bytes", ctypes.c_uint64)]
+
+
+class MoeNode(ctypes.Structure):
+    pass
+
+
+MoeNode._fields_ = [("op", ctypes.c_int32), ("type", ctypes.c_int32), ("ne", ctypes.c_int64 * 4),
+                    ("contiguous", ctypes.c_int32), ("in_moe_buffer", ctypes.c_int32), ("glu_op", ctypes.c_int32),
+                    ("glu_swapped", ctypes.c_int32), ("clamp_min", ctypes.c_float), ("clamp_max", ctypes.c_float),
+                    ("src", ctypes.POINTER(MoeNode) * 3), ("view_src", ctypes.POINTER(MoeNode)),
+                    ("data", ctypes.c_void_p), ("name", ctypes.c_char_p)]
+
+
+class MoeSplit(ctypes.Structure):
+    _fields_ = [(n, ctypes.POINTER(MoeNode)) for n in ("gate_w", "up_w", "down_w", "x", "ids", "wts", "out")] + \
+               [(n, ctypes.c_float) for n in ("gate_min", "gate_max", "up_min", "up_max")] + \
+               [(n, ctypes.c_int32) for n in ("layer", "n_slots", "n_tokens", "hidden", "ffn", "n_expert")]
 
 
 class KernelStat(ctypes.Structure):
@@ -193,11 +216,41 @@ def load_library(path: str | None = None):
     L.moe_server_listen.argtypes = [_vp, ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(ctypes.c_int)]
     L.moe_server_serve.restype = st
     L.moe_server_serve.argtypes = [_vp, ctypes.c_int]
+    L.moe_node_claimed.restype = ctypes.c_int
+    L.moe_node_claimed.argtypes = [ctypes.POINTER(MoeNode)]
+    L.moe_split_parse.restype = st
+    L.moe_split_parse.argtypes = [ctypes.POINTER(ctypes.POINTER(MoeNode)), ctypes.c_int, ctypes.POINTER(MoeSplit),
+                                  ctypes.c_char_p, ctypes.c_size_t]
+    L.moe_split_compute.restype = st
+    L.moe_split_compute.argtypes = [_vp, ctypes.POINTER(ctypes.POINTER(MoeNode)), ctypes.c_int]
     L.moe_router_logits.restype = st
     L.moe_router_logits.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]
     if path is None:
         _lib = L
     return L
+
+
+def node_list(nodes):
+    """A C array of pointers to MoeNode structures (the caller keeps them alive)."""
+    arr = (ctypes.POINTER(MoeNode) * len(nodes))()
+    for i, nd in enumerate(nodes):
+        arr[i] = ctypes.pointer(nd)
+    return arr
+
+
+def node_claimed(node: MoeNode) -> bool:
+    return bool(load_library().moe_node_claimed(ctypes.byref(node)))
+
+
+def split_parse(nodes) -> MoeSplit:
+    """Parse the routed-expert split; raises MoeError (MOE_ERR_UNSUPPORTED with the reason)."""
+    L = load_library()
+    sp = MoeSplit()
+    why = ctypes.create_string_buffer(256)
+    st = L.moe_split_parse(node_list(nodes), len(nodes), ctypes.byref(sp), why, len(why))
+    if st != MOE_OK:
+        raise MoeError(st, f"moe_split_parse: {why.value.decode()}")
+    return sp
 
 
 def read_gguf_layer(path: str, layer: int) -> GgufLayer:
@@ -356,6 +409,10 @@ class MoeBlock:
         self._check(self.lib.moe_route_forward(self.h, layer, _ptr(x), _ptr(logits), _ptr(bias), T, mode,
                                                int(norm), scale, _ptr(ids), _ptr(wts), _ptr(out), flags,
                                                _stream(stream)), "moe_route_forward")
+
+    def split_compute(self, nodes):
+        """Compute a parsed split (moe_split_compute) into its MUL node's host data."""
+        self._check(self.lib.moe_split_compute(self.h, node_list(nodes), len(nodes)), "moe_split_compute")
 
     def forward_host(self, layer: int, x: np.ndarray, ids: np.ndarray, wts: np.ndarray,
                      flags: int = 0) -> np.ndarray:

@@ -407,6 +407,60 @@ def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
     g.close()
 
 
+# ---- the ggml backend's split, computed through moe_split_compute -----------------------------
+
+@pytest.mark.parametrize("T", [1, 5])
+def test_split_compute_c1(blk, oracle, c1, T):
+    """The routed-expert block graph of layer 1 (tests/split_graph.py) computed
+    through the split interface: the MUL node's data equals the block's
+    per-slot output bit for bit; a split whose clamps are not the layer's,
+    and one for a layer that is not resident, are refused for the CPU path."""
+    import split_graph as sg
+    H, F, E, k = c1.hidden, c1.ffn, c1.n_expert, c1.n_used
+    x, lg = wl.make_inputs(c1, T, 60 + T)
+    ids, wts = oracle.route(lg, k, c1.route_mode, norm=True)
+    out = np.full((T, k, H), np.nan, np.float32)
+    g, nd = sg.block(H, F, E, k, T, 1, x=x, ids=ids, wts=wts, out=out)
+    say("split compute, C1 layer 1, T", T)
+    blk.split_compute(sg.split_nodes(g, nd))
+    ref = blk.forward_host(1, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
+    assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+    g2, nd2 = sg.block(H, F, E, k, T, 1, clamp=5.0, x=x, ids=ids, wts=wts)
+    with pytest.raises(mb.MoeError) as ei:
+        blk.split_compute(sg.split_nodes(g2, nd2))
+    assert ei.value.status == mb.MOE_ERR_UNSUPPORTED and "clamps" in str(ei.value)
+    g3, nd3 = sg.block(H, F, E, k, T, 55, x=x, ids=ids, wts=wts)
+    with pytest.raises(mb.MoeError) as ei:
+        blk.split_compute(sg.split_nodes(g3, nd3))
+    assert ei.value.status == mb.MOE_ERR_NOT_RESIDENT
+
+
+def test_split_compute_with_clamps(blk, oracle):
+    """A deepseek4-style split (gate clamped to <= L, up to [-L, L]) on a layer
+    with that clamp, checked against the oracle's MUL node (per-slot rows)."""
+    import split_graph as sg
+    shape = wl.LayerShape(hidden=1024, ffn=512, n_expert=16, n_used=4, has_shared=False,
+                          route_mode=wl.ROUTE_SIGMOID, clamp=0.75)
+    blk.generate_layer(8, shape, seed=57, e_lo=128, e_span=3)
+    try:
+        T = 3
+        x, lg = wl.make_inputs(shape, T, 33)
+        ids, wts = oracle.route(lg, shape.n_used, shape.route_mode, norm=True)
+        out = np.zeros((T, shape.n_used, shape.hidden), np.float32)
+        g, nd = sg.block(shape.hidden, shape.ffn, shape.n_expert, shape.n_used, T, 8, clamp=0.75, x=x, ids=ids,
+                         wts=wts, out=out)
+        blk.split_compute(sg.split_nodes(g, nd))
+        ref = blk.forward_host(8, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
+        assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
+        # a sanity bound only: the block's own parity (with Q8_0 boundary tokens
+        # handled) is test_clamp_active's; this split equals the block bit for bit
+        L = oracle_layer(oracle, shape, 57, 8, ids, e_lo=128, e_span=3)
+        o = L.forward(x, ids, wts, per_slot=True)["per_slot"]
+        assert_rms_close(out, o, tol=2e-2, what="split with clamps vs oracle MUL node")
+    finally:
+        blk.release_layer(8)
+
+
 # ---- a layer read from a GGUF model ----------------------------------------------------------
 
 @pytest.mark.parametrize("T", [1, 6])
