@@ -407,6 +407,44 @@ def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
     g.close()
 
 
+# ---- shapes beyond the configs: every kernel variant against the oracle ----------------------
+
+# (H, F, E, k, T, shared, clamp, route): chosen so that each dispatch branch runs at
+# least once off the configs' shapes: decode k_gate_up<1> (narrow) / k_gate_up_bal2
+# (9-task workgroups) / k_gate_up_bal (other task counts); pairs (T <= 4); octets with
+# k_gate_up_o and with k_gate_up_o2 (P >= 2E, H = 256 * {8, 16, 28}); k_down_ol<6, 8,
+# 16, 28> and k_down_o (F / 128 without an instance); shared expert and clamp on and off.
+SWEEP = [
+    (3072, 768, 32, 4, 1, False, 0.0, wl.ROUTE_SOFTMAX),      # decode, narrow: k_gate_up<1>
+    (2048, 2048, 64, 8, 1, True, 0.0, wl.ROUTE_SIGMOID),      # decode, 256 workgroups: bal2
+    (1024, 2048, 16, 5, 1, False, 4.0, wl.ROUTE_SIGMOID),     # decode, 1280 tasks: k_gate_up_bal
+    (1024, 3584, 8, 2, 3, False, 0.0, wl.ROUTE_SOFTMAX),      # pairs, F = 3584
+    (4096, 1024, 64, 6, 32, True, 0.0, wl.ROUTE_SIGMOID),     # octets, o2<16>, k_down_ol<8>
+    (2048, 1536, 16, 2, 20, False, 6.0, wl.ROUTE_SOFTMAX),    # octets, o2<8>, k_down_o
+    (1024, 1024, 256, 8, 7, True, 0.0, wl.ROUTE_SIGMOID),     # octets, k_gate_up_o, k_down_ol<8>
+    (7168, 768, 16, 4, 9, False, 0.0, wl.ROUTE_SQRT_SOFTPLUS),  # o2<28>, 16-row items, k_down_ol<6>
+    (2048, 3584, 8, 2, 33, True, 8.0, wl.ROUTE_SIGMOID),      # o2<8>, k_down_ol<28>, clamp
+]
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("case", range(len(SWEEP)))
+def test_shape_sweep(blk, torch_dev, oracle, case):
+    H, F, E, k, T, sh, clamp, route = SWEEP[case]
+    shape = wl.LayerShape(hidden=H, ffn=F, n_expert=E, n_used=k, has_shared=sh, route_mode=route, clamp=clamp)
+    say(f"sweep case {case}: H={H} F={F} E={E} k={k} T={T} shared={sh} clamp={clamp} route={route}")
+    lid = 300 + case
+    blk.generate_layer(lid, shape, seed=900 + case)
+    try:
+        x, lg = wl.make_inputs(shape, T, 70 + case)
+        ids, wts = oracle.route(lg, k, route, norm=True)
+        got = run_block(blk, torch_dev, lid, x, ids, wts)
+        check_block(oracle, oracle_layer(oracle, shape, 900 + case, lid, ids), blk, shape, x, ids, wts, got,
+                    f"sweep {case}")
+    finally:
+        blk.release_layer(lid)
+
+
 # ---- the ggml backend's split, computed through moe_split_compute -----------------------------
 
 @pytest.mark.parametrize("T", [1, 5])
