@@ -361,10 +361,13 @@ def test_c4_prefill_chunk(blk, torch_dev, oracle, v3, zipf):
     check_block(oracle, L, blk_sub, v3, x[sub], ids[sub], wts[sub], got[sub], "C4")
 
 
-def test_graph_replay_grouped(blk, torch_dev, oracle, v3):
-    """A T=16 grouped call captured in a graph: every replay equals the eager call."""
+@pytest.mark.parametrize("T", [16, 64])
+def test_graph_replay_grouped(blk, torch_dev, oracle, v3, T):
+    """A grouped call captured in a graph (T=16: k_gate_up_o on the 8-row items;
+    T=64: k_gate_up_o2 on the second, 16-row item list): every replay equals
+    the eager call."""
     torch, dev = torch_dev
-    T = 16
+    say("graph capture grouped T", T)
     blk.reserve(v3, T)
     x, lg = wl.make_inputs(v3, T, 77, zipf=True)
     ids, wts = oracle.route(lg, 8, v3.route_mode, norm=True)
