@@ -51,10 +51,10 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cpus))")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the hipGraph")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "boundary"],
                     help="c2 (default): the headline V3 decode line; c1/c3/c4/c5: one line per measured case of "
                          "that configuration (C1 decode, C3 T=4/16/64 Zipf, C4 T=512 uniform and Zipf, C5 40-layer "
-                         "graph)")
+                         "graph); boundary: V3 decode calls through the host-buffer split interface")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB three times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
@@ -305,6 +305,140 @@ def bench_config(args):
     blk.close()
 
 
+def bench_boundary(args):
+    """V3 decode (T=1) through the ggml backend's host boundary: a split of
+    moe_node structures over host buffers (x, ids, wts in; the MUL node's
+    [k][H] rows out) computed by moe_split_compute, which parses it, copies
+    the inputs to the device, runs the block and copies the rows back.  Each
+    call is timed on the host clock from the call to its return; the calls
+    cycle over --layers resident layers with their own tokens and routing.
+    The same calls through moe_forward_host (no parse) and the device-side
+    forward alone are timed beside it.  The reference's per-call cost at this
+    boundary is moe_tp_compute's: 439 us per layer, ~113 us of it GPU time
+    (moe-serv MEASUREMENTS.md:108-111, V4-Flash on its own hardware, so no
+    vs_baseline)."""
+    import ctypes
+
+    import numpy as np
+    import torch
+
+    import moe_block as mb
+    import workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    sh = wl.V3
+    NL = args.layers
+    H, F, E, k = sh.hidden, sh.ffn, sh.n_expert, sh.n_used
+    blk = mb.MoeBlock(0)
+    for layer in range(NL):
+        blk.generate_layer(layer, sh, seed=args.seed + layer)
+    n = max(args.steps, 64)
+    x_np, lg_np = wl.make_inputs(sh, n, args.seed + 11)
+    ids_d = torch.empty((n, k), dtype=torch.int32, device=dev)
+    wts_d = torch.empty((n, k), dtype=torch.float32, device=dev)
+    blk.route(torch.from_numpy(lg_np).to(dev), k, sh.route_mode, sh.norm, sh.scale, ids_d, wts_d)
+    torch.cuda.synchronize()
+    ids_np, wts_np = ids_d.cpu().numpy(), wts_d.cpu().numpy()
+    keep = []
+
+    def node(op, ne, type_=mb.GGML_F32, src=(), data=None, name=None, ours=False, **kw):
+        nd = mb.MoeNode()
+        nd.op, nd.type, nd.contiguous, nd.in_moe_buffer = op, type_, 1, int(ours)
+        for i, v in enumerate(list(ne) + [1] * (4 - len(ne))):
+            nd.ne[i] = v
+        nd.glu_op = kw.get("glu_op", 0)
+        for i, sn in enumerate(src):
+            nd.src[i] = ctypes.pointer(sn)
+        if data is not None:
+            nd.data = data.ctypes.data
+            keep.append(data)
+        if name is not None:
+            b = name.encode()
+            keep.append(b)
+            nd.name = b
+        keep.append(nd)
+        return nd
+
+    splits, outs = [], []
+    for i in range(n):  # the block's nodes as ggml builds them (no clamps: V3)
+        layer = i % NL
+        xi = np.ascontiguousarray(x_np[i:i + 1])
+        idi, wti = np.ascontiguousarray(ids_np[i:i + 1]), np.ascontiguousarray(wts_np[i:i + 1])
+        oi = np.empty((1, k, H), np.float32)
+        oi.fill(0.0)  # pages touched, as a graph allocator's reused buffer would be
+        b = f"blk.{layer}."
+        wg = node(mb.NODE_NONE, (H, F, E), mb.GGML_MXFP4, name=b + "ffn_gate_exps.weight", ours=True)
+        wu = node(mb.NODE_NONE, (H, F, E), mb.GGML_MXFP4, name=b + "ffn_up_exps.weight", ours=True)
+        wd = node(mb.NODE_NONE, (F, H, E), mb.GGML_MXFP4, name=b + "ffn_down_exps.weight", ours=True)
+        xn = node(mb.NODE_NONE, (H, 1, 1), data=xi)
+        idn = node(mb.NODE_NONE, (k, 1), mb.GGML_I32, data=idi)
+        wn = node(mb.NODE_NONE, (1, k, 1), data=wti)
+        up = node(mb.NODE_MUL_MAT_ID, (F, k, 1), src=(wu, xn, idn))
+        gate = node(mb.NODE_MUL_MAT_ID, (F, k, 1), src=(wg, xn, idn))
+        act = node(mb.NODE_GLU, (F, k, 1), src=(gate, up), glu_op=mb.GLU_SWIGLU)
+        y = node(mb.NODE_MUL_MAT_ID, (H, k, 1), src=(wd, act, idn))
+        mul = node(mb.NODE_MUL, (H, k, 1), src=(y, wn), data=oi)
+        splits.append(mb.node_list([up, gate, act, y, mul]))
+        outs.append(oi)
+    lib = blk.lib
+    W = min(args.warmup, n)
+
+    def timed(call):
+        for i in range(W):
+            call(i)
+        ts = []
+        for i in range(n):
+            t0 = time.perf_counter()
+            call(i)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts)) * 1e6, float(np.mean(ts)) * 1e6
+
+    def via_split(i):
+        st = lib.moe_split_compute(blk.h, splits[i], 5)
+        if st != mb.MOE_OK:
+            raise SystemExit(f"bench: moe_split_compute failed ({st})")
+
+    ref = np.empty((1, k, H), np.float32)
+
+    def via_host(i):
+        st = lib.moe_forward_host(blk.h, i % NL, x_np[i:i + 1].ctypes.data, ids_np[i:i + 1].ctypes.data,
+                                  wts_np[i:i + 1].ctypes.data, 1, ref.ctypes.data, mb.MOE_FWD_PER_SLOT)
+        if st != mb.MOE_OK:
+            raise SystemExit(f"bench: moe_forward_host failed ({st})")
+
+    xd = torch.from_numpy(x_np).to(dev)
+    od = torch.empty((1, k, H), dtype=torch.float32, device=dev)
+
+    def device_only(i):
+        blk.forward(i % NL, xd[i:i + 1], ids_d[i:i + 1], wts_d[i:i + 1], od, mb.MOE_FWD_PER_SLOT)
+        torch.cuda.synchronize()
+
+    med_s, mean_s = timed(via_split)
+    med_h, mean_h = timed(via_host)
+    med_d, mean_d = timed(device_only)
+    via_host(n - 1)
+    if not np.array_equal(outs[n - 1].view(np.uint32), ref.view(np.uint32)):
+        raise SystemExit("bench: split and forward_host outputs differ")
+    line = {
+        "metric": "MoE-layer us/call through the host split boundary (x, ids, wts in; MUL node out)",
+        "value": round(med_s, 2), "unit": "us/call", "n_gpus": 1, "steps": n, "warmup": W,
+        "higher_is_better": False, "dtype": "mxfp4 x q8_0, f32 accumulate", "data": "synthetic",
+        "config": {"workload": "V3 decode T=1 via moe_split_compute (per-slot MUL node, no shared expert), "
+                               f"{NL} resident layers cycled", "timed_as": "host clock per call, median"},
+        "mean_us": round(mean_s, 2),
+        "forward_host_us_median": round(med_h, 2),
+        "device_forward_us_median": round(med_d, 2),
+        "reference_us_per_layer": {"moe_tp_compute": 439, "of_which_gpu": 113,
+                                   "source": "moe-serv MEASUREMENTS.md:108-111 (V4-Flash, other hardware)"},
+        "vs_baseline": None,
+    }
+    log(f"split boundary: {med_s:.1f} us/call median ({mean_s:.1f} mean); forward_host {med_h:.1f}; "
+        f"device forward + sync {med_d:.1f}")
+    print(json.dumps(line), flush=True)
+    blk.close()
+
+
 def main():
     args = parse()
     if args.copy_mib > 0:
@@ -315,6 +449,9 @@ def main():
               f"sharding of the block is design-only", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "boundary":
+        bench_boundary(args)
+        return
     if args.workload != "c2":
         bench_config(args)
         return

@@ -56,10 +56,11 @@ struct scratch {
   float *part = nullptr; int *tick = nullptr;
   int32_t *grp = nullptr;                          // grouping workspace
   size_t grp_words = 0;
-  // split-K decode: chunk partial sums and per-unit tickets (the tickets are
-  // zeroed once here and left at zero by every launch)
   // host-boundary staging
-  float *x_in = nullptr; int32_t *ids_in = nullptr; float *wts_in = nullptr; float *out_buf = nullptr;
+  // one allocation for the three inputs, laid out as moe_forward_host's pinned
+  // staging (ids at 0, wts at in_wts, x at in_x bytes) so one copy moves them
+  int32_t *ids_in = nullptr; float *wts_in = nullptr; float *x_in = nullptr; float *out_buf = nullptr;
+  size_t in_wts = 0, in_x = 0;
   size_t out_cap = 0;
   size_t h_rows = 0;     // rows written to htap by the last forward
   int last_F = 0;
@@ -95,6 +96,9 @@ struct moe_ctx {
   bool capturing = false;
   bool taps = false;  // keep the SwiGLU output h in sc.htap (moe_debug_set_taps)
   prof_state prof;
+  // moe_forward_host's pinned staging (x, ids, wts in; out back), grown on demand
+  uint8_t *pin = nullptr;
+  size_t pin_bytes = 0;
 };
 
 // HIP-event pair around one kernel launch while profiling is on (never
@@ -195,8 +199,7 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 // scratch
 
 static void scratch_free(scratch &s) {
-  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.part, s.tick, s.grp, s.x_in, s.ids_in, s.wts_in,
-                  s.out_buf};
+  void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.part, s.tick, s.grp, s.ids_in, s.out_buf};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
   s = scratch();
@@ -225,9 +228,11 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
   HIPC(c, hipMemset(s.tick, 0, (size_t)16 * (F / 32) * 4));
   s.grp_words = group_ws_words(T, k, E);
   HIPC(c, hipMalloc(&s.grp, s.grp_words * 4));
-  HIPC(c, hipMalloc(&s.x_in, (size_t)T * H * 4));
-  HIPC(c, hipMalloc(&s.ids_in, P * 4));
-  HIPC(c, hipMalloc(&s.wts_in, P * 4));
+  s.in_wts = P * 4;
+  s.in_x = (2 * P * 4 + 255) & ~(size_t)255;
+  HIPC(c, hipMalloc(&s.ids_in, s.in_x + (size_t)T * H * 4));
+  s.wts_in = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(s.ids_in) + s.in_wts);
+  s.x_in = reinterpret_cast<float *>(reinterpret_cast<uint8_t *>(s.ids_in) + s.in_x);
   s.out_cap = P * H;
   HIPC(c, hipMalloc(&s.out_buf, s.out_cap * 4));
   HIPC(c, hipDeviceSynchronize());
@@ -272,6 +277,7 @@ extern "C" void moe_ctx_destroy(moe_ctx *c) {
     for (dev_mat &m : kv.second.m)
       if (m.w) (void)hipFree(m.w);
   scratch_free(c->sc);
+  if (c->pin) (void)hipHostFree(c->pin);
   for (auto &r : c->prof.pending) {
     (void)hipEventDestroy(r.a);
     (void)hipEventDestroy(r.b);
@@ -780,12 +786,31 @@ extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, co
   scratch &s = c->sc;
   const size_t P = (size_t)T * d.n_used;
   const size_t n_out = (flags & MOE_FWD_PER_SLOT) ? P * d.hidden : (size_t)T * d.hidden;
-  HIPC(c, hipMemcpy(s.x_in, x, (size_t)T * d.hidden * 4, hipMemcpyHostToDevice));
-  HIPC(c, hipMemcpy(s.ids_in, ids, P * 4, hipMemcpyHostToDevice));
-  HIPC(c, hipMemcpy(s.wts_in, wts, P * 4, hipMemcpyHostToDevice));
+  // the caller's buffers are pageable: stage them through one pinned buffer in
+  // the device layout of the inputs (host memcpy, then one asynchronous copy
+  // in and one out), cheaper than a staged copy per array
+  const size_t bx = (size_t)T * d.hidden * 4, bi = P * 4, bo = n_out * 4, bin = s.in_x + bx;
+  const size_t need = ((bin + 255) & ~(size_t)255) + bo;
+  if (c->pin_bytes < need) {
+    if (c->pin) (void)hipHostFree(c->pin);
+    c->pin = nullptr;
+    c->pin_bytes = 0;
+    HIPC(c, hipHostMalloc((void **)&c->pin, need, hipHostMallocDefault));
+    c->pin_bytes = need;
+  }
+  uint8_t *pin_out = c->pin + ((bin + 255) & ~(size_t)255);
+  memcpy(c->pin, ids, bi);
+  memcpy(c->pin + s.in_wts, wts, bi);
+  memcpy(c->pin + s.in_x, x, bx);
+  HIPC(c, hipMemcpyAsync(s.ids_in, c->pin, bin, hipMemcpyHostToDevice, nullptr));
   st = moe_forward(c, layer, s.x_in, s.ids_in, s.wts_in, T, s.out_buf, flags, nullptr);
-  if (st != MOE_OK) return st;
-  HIPC(c, hipMemcpy(out, s.out_buf, n_out * 4, hipMemcpyDeviceToHost));
+  if (st != MOE_OK) {
+    (void)hipStreamSynchronize(nullptr);  // the staging copies finish before the next call reuses the buffer
+    return st;
+  }
+  HIPC(c, hipMemcpyAsync(pin_out, s.out_buf, bo, hipMemcpyDeviceToHost, nullptr));
+  HIPC(c, hipStreamSynchronize(nullptr));
+  memcpy(out, pin_out, bo);
   return MOE_OK;
 }
 
