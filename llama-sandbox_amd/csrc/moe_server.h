@@ -43,14 +43,16 @@ struct moe_server {
   size_t cap_tokens = 0;
   float *x = nullptr, *logits = nullptr, *wts = nullptr, *out = nullptr;
   int32_t *ids = nullptr;
-  std::vector<float> host_out;
+  float *pin_x = nullptr, *pin_out = nullptr;  // pinned host staging of x and the rows
   int listen_fd = -1;
 };
 
 static void srv_free_buffers(moe_server *s) {
   for (void *p : {(void *)s->x, (void *)s->logits, (void *)s->wts, (void *)s->out, (void *)s->ids})
     if (p) (void)hipFree(p);
-  s->x = s->logits = s->wts = s->out = nullptr;
+  for (void *p : {(void *)s->pin_x, (void *)s->pin_out})
+    if (p) (void)hipHostFree(p);
+  s->x = s->logits = s->wts = s->out = s->pin_x = s->pin_out = nullptr;
   s->ids = nullptr;
   s->cap_tokens = 0;
 }
@@ -258,7 +260,9 @@ static bool srv_reserve(moe_server *s, size_t T) {
   const size_t H = s->n_embd, E = s->n_expert, k = s->n_used;
   if (hipMalloc(&s->x, T * H * 4) != hipSuccess || hipMalloc(&s->out, T * H * 4) != hipSuccess ||
       hipMalloc(&s->logits, T * E * 4) != hipSuccess || hipMalloc(&s->wts, T * k * 4) != hipSuccess ||
-      hipMalloc(&s->ids, T * k * 4) != hipSuccess) {
+      hipMalloc(&s->ids, T * k * 4) != hipSuccess ||
+      hipHostMalloc((void **)&s->pin_x, T * H * 4, hipHostMallocDefault) != hipSuccess ||
+      hipHostMalloc((void **)&s->pin_out, T * H * 4, hipHostMallocDefault) != hipSuccess) {
     srv_free_buffers(s);
     return false;
   }
@@ -266,26 +270,27 @@ static bool srv_reserve(moe_server *s, size_t T) {
   return true;
 }
 
-// A checked request with its payload: route, evaluate, respond.  False: an
-// error response was produced (the connection closes).
-static bool srv_eval(moe_server *s, const moe_wire_request &rq, const float *x, uint32_t t_parse_us,
+// A checked request with its payload x (in s->pin_x already, or anywhere in
+// host memory): route, evaluate, respond.  False: an error response was
+// produced (the connection closes).
+static bool srv_eval(moe_server *s, const moe_wire_request &rq, const void *x, uint32_t t_parse_us,
                      std::vector<uint8_t> &resp) {
   const srv_layer &L = s->layers[rq.layer];
   const int T = (int)rq.n_tokens, H = (int)s->n_embd, E = (int)s->n_expert, k = (int)s->n_used;
   const size_t n = (size_t)T * H;
   const auto t0 = srv_clk::now();
-  bool ok = hipSetDevice(s->device) == hipSuccess && srv_reserve(s, (size_t)T) &&
-            hipMemcpyAsync(s->x, x, n * 4, hipMemcpyHostToDevice, s->stream) == hipSuccess &&
+  bool ok = hipSetDevice(s->device) == hipSuccess && srv_reserve(s, (size_t)T);
+  if (ok && x != s->pin_x) memcpy(s->pin_x, x, n * 4);
+  ok = ok && hipMemcpyAsync(s->x, s->pin_x, n * 4, hipMemcpyHostToDevice, s->stream) == hipSuccess &&
             moe_router_logits(s->ctx, L.w, s->x, T, E, H, s->logits, s->stream) == MOE_OK &&
             moe_route(s->ctx, s->logits, L.bias, T, E, k, L.route_mode, L.route_norm, L.route_scale, s->ids, s->wts,
                       s->stream) == MOE_OK &&
             hipStreamSynchronize(s->stream) == hipSuccess;
   const uint32_t t_route_us = srv_us(t0);
   const auto t1 = srv_clk::now();
-  s->host_out.resize(n);
   ok = ok &&
        moe_forward(s->ctx, (int)rq.layer, s->x, s->ids, s->wts, T, s->out, MOE_FWD_NO_SHARED, s->stream) == MOE_OK &&
-       hipMemcpyAsync(s->host_out.data(), s->out, n * 4, hipMemcpyDeviceToHost, s->stream) == hipSuccess &&
+       hipMemcpyAsync(s->pin_out, s->out, n * 4, hipMemcpyDeviceToHost, s->stream) == hipSuccess &&
        hipStreamSynchronize(s->stream) == hipSuccess;
   const uint32_t t_compute_us = srv_us(t1);
   if (!ok) {
@@ -307,7 +312,7 @@ static bool srv_eval(moe_server *s, const moe_wire_request &rq, const float *x, 
   rh.t_compute_us = t_compute_us;
   rh.payload_bytes = n * 4;
   resp.resize(sizeof(rh) + n * 4);
-  memcpy(resp.data() + sizeof(rh), s->host_out.data(), n * 4);
+  memcpy(resp.data() + sizeof(rh), s->pin_out, n * 4);
   rh.t_serialize_us = srv_us(t2);
   memcpy(resp.data(), &rh, sizeof(rh));
   return true;
@@ -337,9 +342,7 @@ extern "C" moe_status moe_server_handle(moe_server *s, const void *msg, size_t l
     } else if (len - sizeof(rq) != rq.payload_bytes) {
       srv_error(r, MOE_WIRE_ERR_DIMS, "payload_bytes does not match the message");
     } else {
-      std::vector<float> x(rq.payload_bytes / 4);
-      memcpy(x.data(), m + sizeof(rq), rq.payload_bytes);
-      srv_eval(s, rq, x.data(), srv_us(t0), r);
+      srv_eval(s, rq, m + sizeof(rq), srv_us(t0), r);
     }
   }
   *resp_len = r.size();
@@ -413,7 +416,6 @@ static void srv_connection(moe_server *s, int fd) {
     if (!srv_recv_all(fd, &peer[0], peer.size())) return;
   }
   if (!srv_send_all(fd, resp.data(), resp.size()) || !hello_ok) return;
-  std::vector<float> x;
   for (;;) {
     moe_wire_request rq;
     if (!srv_recv_all(fd, &rq, sizeof(rq))) return;
@@ -426,9 +428,13 @@ static void srv_connection(moe_server *s, int fd) {
       return;  // the stream position is no longer trusted
     }
     const uint32_t t_parse_us = srv_us(t0);
-    x.resize(rq.payload_bytes / 4);
-    if (!srv_recv_all(fd, x.data(), rq.payload_bytes)) return;
-    const bool ok = srv_eval(s, rq, x.data(), t_parse_us, resp);
+    if (hipSetDevice(s->device) != hipSuccess || !srv_reserve(s, rq.n_tokens)) {
+      srv_error(resp, MOE_WIRE_ERR_INTERNAL, "out of memory for the request");
+      srv_send_all(fd, resp.data(), resp.size());
+      return;
+    }
+    if (!srv_recv_all(fd, s->pin_x, rq.payload_bytes)) return;  // straight into the pinned staging
+    const bool ok = srv_eval(s, rq, s->pin_x, t_parse_us, resp);
     if (!srv_send_all(fd, resp.data(), resp.size()) || !ok) return;
   }
 }
