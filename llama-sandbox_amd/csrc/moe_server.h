@@ -44,6 +44,7 @@ struct moe_server {
   float *x = nullptr, *logits = nullptr, *wts = nullptr, *out = nullptr;
   int32_t *ids = nullptr;
   float *pin_x = nullptr, *pin_out = nullptr;  // pinned host staging of x and the rows
+  hipEvent_t ev[3] = {nullptr, nullptr, nullptr};  // request start, routed, evaluated
   int listen_fd = -1;
 };
 
@@ -67,6 +68,8 @@ extern "C" void moe_server_close(moe_server *s) {
     if (l.w) (void)hipFree(l.w);
     if (l.bias) (void)hipFree(l.bias);
   }
+  for (hipEvent_t e : s->ev)
+    if (e) (void)hipEventDestroy(e);
   if (s->stream) (void)hipStreamDestroy(s->stream);
   if (s->ctx) moe_ctx_destroy(s->ctx);
   delete s;
@@ -128,7 +131,9 @@ static moe_status server_open(moe_server *s, const char *path, uint64_t budget) 
   s->n_dense_lead = M.get_int(a + "leading_dense_block_count", &v) && v >= 0 ? (uint32_t)v : 0;
   const int64_t n_hash = M.get_int(a + "hash_layer_count", &v) && v > 0 ? v : 0;
   s->layers.resize(s->n_layer);
-  if (hipSetDevice(s->device) != hipSuccess || hipStreamCreate(&s->stream) != hipSuccess) {
+  if (hipSetDevice(s->device) != hipSuccess || hipStreamCreate(&s->stream) != hipSuccess ||
+      hipEventCreate(&s->ev[0]) != hipSuccess || hipEventCreate(&s->ev[1]) != hipSuccess ||
+      hipEventCreate(&s->ev[2]) != hipSuccess) {
     return srv_fail(s, MOE_ERR_HIP, "stream creation failed");
   }
   for (uint32_t il = s->n_dense_lead; il < s->n_layer; il++) {
@@ -278,21 +283,25 @@ static bool srv_eval(moe_server *s, const moe_wire_request &rq, const void *x, u
   const srv_layer &L = s->layers[rq.layer];
   const int T = (int)rq.n_tokens, H = (int)s->n_embd, E = (int)s->n_expert, k = (int)s->n_used;
   const size_t n = (size_t)T * H;
-  const auto t0 = srv_clk::now();
+  // route and evaluate back to back on the stream; the two phases are timed
+  // with events (no host round trip between them)
   bool ok = hipSetDevice(s->device) == hipSuccess && srv_reserve(s, (size_t)T);
   if (ok && x != s->pin_x) memcpy(s->pin_x, x, n * 4);
-  ok = ok && hipMemcpyAsync(s->x, s->pin_x, n * 4, hipMemcpyHostToDevice, s->stream) == hipSuccess &&
-            moe_router_logits(s->ctx, L.w, s->x, T, E, H, s->logits, s->stream) == MOE_OK &&
-            moe_route(s->ctx, s->logits, L.bias, T, E, k, L.route_mode, L.route_norm, L.route_scale, s->ids, s->wts,
-                      s->stream) == MOE_OK &&
-            hipStreamSynchronize(s->stream) == hipSuccess;
-  const uint32_t t_route_us = srv_us(t0);
-  const auto t1 = srv_clk::now();
-  ok = ok &&
+  ok = ok && hipEventRecord(s->ev[0], s->stream) == hipSuccess &&
+       hipMemcpyAsync(s->x, s->pin_x, n * 4, hipMemcpyHostToDevice, s->stream) == hipSuccess &&
+       moe_router_logits(s->ctx, L.w, s->x, T, E, H, s->logits, s->stream) == MOE_OK &&
+       moe_route(s->ctx, s->logits, L.bias, T, E, k, L.route_mode, L.route_norm, L.route_scale, s->ids, s->wts,
+                 s->stream) == MOE_OK &&
+       hipEventRecord(s->ev[1], s->stream) == hipSuccess &&
        moe_forward(s->ctx, (int)rq.layer, s->x, s->ids, s->wts, T, s->out, MOE_FWD_NO_SHARED, s->stream) == MOE_OK &&
        hipMemcpyAsync(s->pin_out, s->out, n * 4, hipMemcpyDeviceToHost, s->stream) == hipSuccess &&
-       hipStreamSynchronize(s->stream) == hipSuccess;
-  const uint32_t t_compute_us = srv_us(t1);
+       hipEventRecord(s->ev[2], s->stream) == hipSuccess && hipStreamSynchronize(s->stream) == hipSuccess;
+  float ms_route = 0.0f, ms_compute = 0.0f;
+  if (ok) {
+    (void)hipEventElapsedTime(&ms_route, s->ev[0], s->ev[1]);
+    (void)hipEventElapsedTime(&ms_compute, s->ev[1], s->ev[2]);
+  }
+  const uint32_t t_route_us = (uint32_t)(ms_route * 1e3f), t_compute_us = (uint32_t)(ms_compute * 1e3f);
   if (!ok) {
     s->err = moe_ctx_last_error(s->ctx);
     srv_error(resp, MOE_WIRE_ERR_INTERNAL, "evaluation failed");
