@@ -51,10 +51,11 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget (0 = skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cpus))")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the hipGraph")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "boundary"],
+    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "boundary", "server"],
                     help="c2 (default): the headline V3 decode line; c1/c3/c4/c5: one line per measured case of "
                          "that configuration (C1 decode, C3 T=4/16/64 Zipf, C4 T=512 uniform and Zipf, C5 40-layer "
-                         "graph); boundary: V3 decode calls through the host-buffer split interface")
+                         "graph); boundary: V3 decode calls through the host-buffer split interface; server: "
+                         "moe-server protocol v2 requests on a V3-shaped GGUF model")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB three times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
@@ -439,6 +440,98 @@ def bench_boundary(args):
     blk.close()
 
 
+def bench_server(args):
+    """nano-glm's moe-server protocol v2 served from the block (moe_server_handle,
+    no socket): a V3-shaped GGUF model (H=7168, F=2048, 16 routed experts per
+    layer in MXFP4, k=8, f32 router, sigmoid gating; 2 MoE layers, ~750 MB,
+    written to a temporary directory with random codes and E8M0 exponents in
+    [124, 130]) and T=1 requests alternating between the layers; host clock per
+    request from the request bytes to the response bytes, median.  The response
+    header's own route / compute durations are reported beside it."""
+    import shutil
+    import struct
+    import tempfile
+
+    import numpy as np
+    import torch
+
+    import moe_block as mb
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    H, F, E, k, NL = 7168, 2048, 16, 8, 2
+    rng = np.random.default_rng(args.seed)
+
+    def mx(rows, K):  # MXFP4 blocks [E][rows][K/32][17]: exponent byte, 16 code bytes
+        b = rng.integers(0, 256, size=(E, rows, K // 32, 17), dtype=np.uint8)
+        b[..., 0] = rng.integers(124, 131, size=(E, rows, K // 32), dtype=np.uint8)
+        return b
+
+    def s_(v):
+        v = v.encode()
+        return struct.pack("<Q", len(v)) + v
+
+    kv = [("general.architecture", 8, "glm-dsa"), ("glm-dsa.block_count", 4, NL + 1),
+          ("glm-dsa.leading_dense_block_count", 4, 1), ("glm-dsa.embedding_length", 4, H),
+          ("glm-dsa.expert_count", 4, E), ("glm-dsa.expert_used_count", 4, k),
+          ("glm-dsa.expert_feed_forward_length", 4, F), ("glm-dsa.expert_gating_func", 4, 2)]
+    tensors = []
+    for il in range(1, NL + 1):
+        b = f"blk.{il}."
+        tensors += [(b + "ffn_gate_exps.weight", [H, F, E], 39, mx(F, H)), (b + "ffn_up_exps.weight", [H, F, E], 39, mx(F, H)),
+                    (b + "ffn_down_exps.weight", [F, H, E], 39, mx(H, F)),
+                    (b + "ffn_gate_inp.weight", [H, E], 0, (rng.standard_normal((E, H)) * 0.05).astype(np.float32))]
+    tmp = tempfile.mkdtemp(prefix="moe_server_bench_")
+    path = os.path.join(tmp, "v3-shaped.gguf")
+    try:
+        with open(path, "wb") as f:  # GGUF v3: header, key/values, tensor infos, aligned data
+            f.write(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv)))
+            for key, t, v in kv:
+                f.write(s_(key) + struct.pack("<I", t) + (s_(v) if t == 8 else struct.pack("<I", v)))
+            off = 0
+            for name, ne, ty, a in tensors:
+                f.write(s_(name) + struct.pack("<I", len(ne)) + b"".join(struct.pack("<Q", d) for d in ne)
+                        + struct.pack("<IQ", ty, off))
+                off = (off + a.nbytes + 31) // 32 * 32
+            f.write(b"\0" * ((-f.tell()) % 32))
+            for name, ne, ty, a in tensors:
+                f.write(a.tobytes())
+                f.write(b"\0" * ((-a.nbytes) % 32))
+        log(f"server model: {os.path.getsize(path) / 1e6:.0f} MB")
+        srv = mb.MoeServer(path, 0)
+        n = max(args.steps, 64)
+        W = min(args.warmup, n)
+        xs = rng.standard_normal((n, H)).astype(np.float32)
+        msgs = [bytes(mb.WireRequest(mb.WIRE_MAGIC, mb.WIRE_VERSION, mb.WIRE_REQUEST, 1 + i % NL, H, 1,
+                                     mb.WIRE_RET_COMBINED, 0, 4 * H)) + xs[i].tobytes() for i in range(n)]
+        for i in range(W):
+            srv.handle(msgs[i])
+        ts, route, comp = [], [], []
+        for i in range(n):
+            t0 = time.perf_counter()
+            r = srv.handle(msgs[i])
+            ts.append(time.perf_counter() - t0)
+            h = mb.WireResponse.from_buffer_copy(r[:56])
+            if h.status != mb.WIRE_OK:
+                raise SystemExit(f"bench: server answered status {h.status}: {r[56:200]}")
+            route.append(h.t_route_us)
+            comp.append(h.t_compute_us)
+        srv.close()
+    finally:
+        shutil.rmtree(tmp, ignore_errors=True)
+    med = float(np.median(ts)) * 1e6
+    line = {
+        "metric": "moe-server request us (T=1, one MoE layer, routed experts combined; handle(), no socket)",
+        "value": round(med, 2), "unit": "us/request", "n_gpus": 1, "steps": n, "warmup": W,
+        "higher_is_better": False, "dtype": "mxfp4 x q8_0, f32 accumulate", "data": "synthetic",
+        "config": {"workload": f"moe-server protocol v2, V3-shaped GGUF model (H={H}, F={F}, {E} routed experts, "
+                               f"k={k}, {NL} MoE layers alternated)", "timed_as": "host clock per request, median"},
+        "t_route_us_median": float(np.median(route)), "t_compute_us_median": float(np.median(comp)),
+        "vs_baseline": None,
+    }
+    log(f"server: {med:.1f} us/request median; route {np.median(route):.0f} us, compute {np.median(comp):.0f} us")
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
     if args.copy_mib > 0:
@@ -451,6 +544,9 @@ def main():
 
     if args.workload == "boundary":
         bench_boundary(args)
+        return
+    if args.workload == "server":
+        bench_server(args)
         return
     if args.workload != "c2":
         bench_config(args)
