@@ -203,6 +203,20 @@ def test_c1_forward_host_boundary(blk, oracle, c1):
     assert_rms_close(got, ref, what="C1 host")
 
 
+def test_forward_host_staging_grows_and_shrinks(blk, torch_dev, oracle, c1):
+    """The host boundary's pinned staging across calls of changing size (T = 1,
+    9, 2, 1; combined and per-slot): each call equals the device-resident
+    forward on the same inputs, bit for bit."""
+    torch, dev = torch_dev
+    for i, (T, flags) in enumerate([(1, 0), (9, 0), (2, mb.MOE_FWD_PER_SLOT), (1, mb.MOE_FWD_PER_SLOT)]):
+        x, lg = wl.make_inputs(c1, T, 140 + i)
+        ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
+        say("forward_host T", T, "flags", flags)
+        got = blk.forward_host(1, x, ids, wts, flags=flags)
+        ref = run_block(blk, torch_dev, 1, x, ids, wts, flags)
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (T, flags)
+
+
 def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
     x, lg = wl.make_inputs(c1, 6, 21, zipf=True)
     ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
