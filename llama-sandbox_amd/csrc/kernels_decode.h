@@ -25,7 +25,6 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
   __shared__ float sel[MOE_ROUTE_MAX_E];
   __shared__ float red_f[4];
   __shared__ double red_d[4];
-  __shared__ int red_i[4];
   __shared__ int picked[64];
   const int t = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const float *l = logits + (size_t)t * E;
@@ -60,32 +59,30 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
   for (int e = tid; e < E; e += 256) sel[e] = bias ? probs[e] + bias[e] : probs[e];
   __syncthreads();
 
-  for (int s = 0; s < k; s++) {
-    float bv = 0.0f;
-    int bi = -1;
-    for (int e = tid; e < E; e += 256) {
-      bool taken = false;
-      for (int q = 0; q < s; q++) taken |= picked[q] == e;
-      if (!taken) argmax_merge(bv, bi, sel[e], e);
+  // top-k by wave 0 alone, with no barrier between rounds: lane l holds the
+  // selection scores of experts l, l + 64, ...; each round every lane offers
+  // its best expert not yet taken, the wave keeps the largest (ties: the lower
+  // id), and the lane holding it marks it taken
+  if (wave == 0) {
+    uint32_t taken = 0;  // bit j: expert lane + 64 j (E <= 1024)
+    const int nj = (E + 63) / 64;
+    for (int s = 0; s < k; s++) {
+      float bv = 0.0f;
+      int bi = -1;
+      for (int j = 0; j < nj; j++) {
+        const int e = lane + 64 * j;
+        if (e < E && !((taken >> j) & 1u)) argmax_merge(bv, bi, sel[e], e);
+      }
+      for (int off = 32; off >= 1; off >>= 1) {
+        const float v2 = __shfl_xor(bv, off);
+        const int i2 = __shfl_xor(bi, off);
+        argmax_merge(bv, bi, v2, i2);
+      }
+      if (bi >= 0 && (bi & 63) == lane) taken |= 1u << (bi >> 6);
+      if (lane == 0) picked[s] = bi >= 0 ? bi : 0;  // only NaN scores leave nothing selectable
     }
-    for (int off = 32; off >= 1; off >>= 1) {
-      const float v2 = __shfl_xor(bv, off);
-      const int i2 = __shfl_xor(bi, off);
-      argmax_merge(bv, bi, v2, i2);
-    }
-    if (lane == 0) {
-      red_f[wave] = bv;
-      red_i[wave] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-      float v = red_f[0];
-      int i = red_i[0];
-      for (int w = 1; w < 4; w++) argmax_merge(v, i, red_f[w], red_i[w]);
-      picked[s] = i >= 0 ? i : 0;  // only NaN scores leave nothing selectable
-    }
-    __syncthreads();
   }
+  __syncthreads();
   if (tid == 0) {
     float w[64];
     for (int s = 0; s < k; s++) w[s] = probs[picked[s]];
