@@ -415,9 +415,19 @@ def bench_boundary(args):
         blk.forward(i % NL, xd[i:i + 1], ids_d[i:i + 1], wts_d[i:i + 1], od, mb.MOE_FWD_PER_SLOT)
         torch.cuda.synchronize()
 
+    lg_d = torch.from_numpy(lg_np).to(dev)
+    ids_r = torch.empty((1, k), dtype=torch.int32, device=dev)
+    wts_r = torch.empty((1, k), dtype=torch.float32, device=dev)
+
+    def route_and_forward(i):  # logits -> ids, weights -> rows, all on the device
+        blk.route_forward(i % NL, xd[i:i + 1], lg_d[i:i + 1], ids_r, wts_r, od, sh.route_mode, norm=sh.norm,
+                          scale=sh.scale, flags=mb.MOE_FWD_PER_SLOT)
+        torch.cuda.synchronize()
+
     med_s, mean_s = timed(via_split)
     med_h, mean_h = timed(via_host)
     med_d, mean_d = timed(device_only)
+    med_r, _ = timed(route_and_forward)
     via_host(n - 1)
     if not np.array_equal(outs[n - 1].view(np.uint32), ref.view(np.uint32)):
         raise SystemExit("bench: split and forward_host outputs differ")
@@ -430,12 +440,13 @@ def bench_boundary(args):
         "mean_us": round(mean_s, 2),
         "forward_host_us_median": round(med_h, 2),
         "device_forward_us_median": round(med_d, 2),
+        "device_route_forward_us_median": round(med_r, 2),
         "reference_us_per_layer": {"moe_tp_compute": 439, "of_which_gpu": 113,
                                    "source": "moe-serv MEASUREMENTS.md:108-111 (V4-Flash, other hardware)"},
         "vs_baseline": None,
     }
     log(f"split boundary: {med_s:.1f} us/call median ({mean_s:.1f} mean); forward_host {med_h:.1f}; "
-        f"device forward + sync {med_d:.1f}")
+        f"device forward + sync {med_d:.1f}; device route + forward + sync {med_r:.1f}")
     print(json.dumps(line), flush=True)
     blk.close()
 
@@ -497,7 +508,10 @@ def bench_server(args):
                 f.write(a.tobytes())
                 f.write(b"\0" * ((-a.nbytes) % 32))
         log(f"server model: {os.path.getsize(path) / 1e6:.0f} MB")
+        t_load = time.perf_counter()
         srv = mb.MoeServer(path, 0)
+        t_load = time.perf_counter() - t_load
+        load_bytes = NL * 3 * E * F * (H // 32) * 17
         n = max(args.steps, 64)
         W = min(args.warmup, n)
         xs = rng.standard_normal((n, H)).astype(np.float32)
@@ -526,9 +540,11 @@ def bench_server(args):
         "config": {"workload": f"moe-server protocol v2, V3-shaped GGUF model (H={H}, F={F}, {E} routed experts, "
                                f"k={k}, {NL} MoE layers alternated)", "timed_as": "host clock per request, median"},
         "t_route_us_median": float(np.median(route)), "t_compute_us_median": float(np.median(comp)),
+        "model_load_s": round(t_load, 3), "model_load_gbps": round(load_bytes / t_load / 1e9, 2),
         "vs_baseline": None,
     }
-    log(f"server: {med:.1f} us/request median; route {np.median(route):.0f} us, compute {np.median(comp):.0f} us")
+    log(f"server: {med:.1f} us/request median; route {np.median(route):.0f} us, compute {np.median(comp):.0f} us; "
+        f"model load {t_load:.2f} s ({load_bytes / t_load / 1e9:.2f} GB/s of MXFP4 experts from the page cache)")
     print(json.dumps(line), flush=True)
 
 

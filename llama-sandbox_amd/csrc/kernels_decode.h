@@ -17,6 +17,53 @@ __device__ __forceinline__ void argmax_merge(float &v, int &i, float v2, int i2)
   }
 }
 
+// Score of one logit for the element-wise score functions (mode 1: sigmoid,
+// 2: sqrt(softplus)); softmax (mode 0) needs the whole row and stays in k_route.
+__device__ __forceinline__ float route_score(float v, int mode) {
+  return mode == 1 ? __fdiv_rn(1.0f, 1.0f + expf(-v)) : sqrtf(v > 20.0f ? v : log1pf(expf(v)));
+}
+
+// Top-k of sel[0..E) by one wave (called by all 64 lanes of it), with no
+// barrier between rounds: lane l holds experts l, l + 64, ...; each round
+// every lane offers its best expert not yet taken, the wave keeps the largest
+// (ties: the lower id), and the lane holding it marks it taken.  picked[s] is
+// written by lane 0.
+__device__ __forceinline__ void route_topk_wave(const float *sel, int E, int k, int *picked, int lane) {
+  uint32_t taken = 0;  // bit j: expert lane + 64 j (E <= 1024)
+  const int nj = (E + 63) / 64;
+  for (int s = 0; s < k; s++) {
+    float bv = 0.0f;
+    int bi = -1;
+    for (int j = 0; j < nj; j++) {
+      const int e = lane + 64 * j;
+      if (e < E && !((taken >> j) & 1u)) argmax_merge(bv, bi, sel[e], e);
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+      const float v2 = __shfl_xor(bv, off);
+      const int i2 = __shfl_xor(bi, off);
+      argmax_merge(bv, bi, v2, i2);
+    }
+    if (bi >= 0 && (bi & 63) == lane) taken |= 1u << (bi >> 6);
+    if (lane == 0) picked[s] = bi >= 0 ? bi : 0;  // only NaN scores leave nothing selectable
+  }
+}
+
+// Weights of the picked experts from the unbiased scores: renorm by
+// max(sum, 2^-14) when norm, then the scale when it is not 0 or 1 (one thread).
+__device__ __forceinline__ void route_weights(const float *probs, const int *picked, int k, int norm, float scale,
+                                              float *w) {
+  for (int s = 0; s < k; s++) w[s] = probs[picked[s]];
+  if (norm) {
+    double sum = 0.0;
+    for (int s = 0; s < k; s++) sum += (double)w[s];
+    float fs = (float)sum;
+    fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
+    for (int s = 0; s < k; s++) w[s] = __fdiv_rn(w[s], fs);
+  }
+  if (scale != 0.0f && scale != 1.0f)
+    for (int s = 0; s < k; s++) w[s] = __fmul_rn(w[s], scale);
+}
+
 __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
                                                const float *__restrict__ bias, int E, int k,
                                                int mode, int norm, float scale,
@@ -47,55 +94,18 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
     __syncthreads();
     const float inv = (float)(1.0 / (((red_d[0] + red_d[1]) + red_d[2]) + red_d[3]));
     for (int e = tid; e < E; e += 256) probs[e] = probs[e] * inv;
-  } else if (mode == 1) {
-    for (int e = tid; e < E; e += 256) probs[e] = __fdiv_rn(1.0f, 1.0f + expf(-l[e]));
   } else {
-    for (int e = tid; e < E; e += 256) {
-      const float v = l[e];
-      probs[e] = sqrtf(v > 20.0f ? v : log1pf(expf(v)));
-    }
+    for (int e = tid; e < E; e += 256) probs[e] = route_score(l[e], mode);
   }
   __syncthreads();
   for (int e = tid; e < E; e += 256) sel[e] = bias ? probs[e] + bias[e] : probs[e];
   __syncthreads();
 
-  // top-k by wave 0 alone, with no barrier between rounds: lane l holds the
-  // selection scores of experts l, l + 64, ...; each round every lane offers
-  // its best expert not yet taken, the wave keeps the largest (ties: the lower
-  // id), and the lane holding it marks it taken
-  if (wave == 0) {
-    uint32_t taken = 0;  // bit j: expert lane + 64 j (E <= 1024)
-    const int nj = (E + 63) / 64;
-    for (int s = 0; s < k; s++) {
-      float bv = 0.0f;
-      int bi = -1;
-      for (int j = 0; j < nj; j++) {
-        const int e = lane + 64 * j;
-        if (e < E && !((taken >> j) & 1u)) argmax_merge(bv, bi, sel[e], e);
-      }
-      for (int off = 32; off >= 1; off >>= 1) {
-        const float v2 = __shfl_xor(bv, off);
-        const int i2 = __shfl_xor(bi, off);
-        argmax_merge(bv, bi, v2, i2);
-      }
-      if (bi >= 0 && (bi & 63) == lane) taken |= 1u << (bi >> 6);
-      if (lane == 0) picked[s] = bi >= 0 ? bi : 0;  // only NaN scores leave nothing selectable
-    }
-  }
+  if (wave == 0) route_topk_wave(sel, E, k, picked, lane);
   __syncthreads();
   if (tid == 0) {
     float w[64];
-    for (int s = 0; s < k; s++) w[s] = probs[picked[s]];
-    if (norm) {
-      double sum = 0.0;
-      for (int s = 0; s < k; s++) sum += (double)w[s];
-      float fs = (float)sum;
-      fs = fs < 6.103515625e-5f ? 6.103515625e-5f : fs;
-      for (int s = 0; s < k; s++) w[s] = __fdiv_rn(w[s], fs);
-    }
-    if (scale != 0.0f && scale != 1.0f) {
-      for (int s = 0; s < k; s++) w[s] = __fmul_rn(w[s], scale);
-    }
+    route_weights(probs, picked, k, norm, scale, w);
     for (int s = 0; s < k; s++) {
       ids[(size_t)t * k + s] = picked[s];
       wts[(size_t)t * k + s] = w[s];

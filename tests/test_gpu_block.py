@@ -343,6 +343,40 @@ def test_c2_route_forward_ids_bit_exact(blk, torch_dev, oracle, v3):
     assert_rms_close(out.cpu().numpy(), ref, what="C2 e2e")
 
 
+@pytest.mark.parametrize("mode, biased, flags", [(wl.ROUTE_SIGMOID, True, 0), (wl.ROUTE_SQRT_SOFTPLUS, False, 0),
+                                                 (wl.ROUTE_SIGMOID, False, mb.MOE_FWD_PER_SLOT)])
+def test_route_forward_decode(blk, torch_dev, oracle, v3, mode, biased, flags):
+    """V3 decode through moe_route_forward with a selection bias, a weight scale
+    and both element-wise score functions: ids equal the oracle's, and ids,
+    weights and output equal moe_route + moe_forward's, bit for bit."""
+    torch, dev = torch_dev
+    x, lg = wl.make_inputs(v3, 1, 17 + mode)
+    bias = (np.random.default_rng(3).standard_normal(v3.n_expert) * 0.05).astype(np.float32) if biased else None
+    say("fused route+forward mode", mode, "bias", biased, "flags", flags)
+    xd, lgd = torch.from_numpy(x).to(dev), torch.from_numpy(lg).to(dev)
+    bd = torch.from_numpy(bias).to(dev) if biased else None
+    shape = (1, 8, v3.hidden) if flags & mb.MOE_FWD_PER_SLOT else (1, v3.hidden)
+    outs, idss, wtss = [], [], []
+    for fused in (True, False):
+        ids = torch.empty((1, 8), dtype=torch.int32, device=dev)
+        wts = torch.empty((1, 8), dtype=torch.float32, device=dev)
+        out = torch.empty(shape, dtype=torch.float32, device=dev)
+        if fused:
+            blk.route_forward(2, xd, lgd, ids, wts, out, mode=mode, norm=True, scale=2.5, bias=bd, flags=flags)
+        else:
+            blk.route(lgd, 8, mode, True, 2.5, ids, wts, bias=bd)
+            blk.forward(2, xd, ids, wts, out, flags)
+        torch.cuda.synchronize()
+        outs.append(out.cpu().numpy())
+        idss.append(ids.cpu().numpy())
+        wtss.append(wts.cpu().numpy())
+    oi, ow = oracle.route(lg, 8, mode, norm=True, scale=2.5, bias=bias)
+    np.testing.assert_array_equal(idss[0], oi)
+    np.testing.assert_array_equal(idss[0], idss[1])
+    assert np.array_equal(wtss[0].view(np.uint32), wtss[1].view(np.uint32))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+
+
 @pytest.mark.slow
 @pytest.mark.parametrize("T", [4, 16, 64])
 def test_c3_small_batch_zipf(blk, torch_dev, oracle, v3, T):
