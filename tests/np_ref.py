@@ -57,7 +57,8 @@ def swiglu(g: np.ndarray, u: np.ndarray, clamp: float) -> np.ndarray:
     if clamp > 1e-6:
         u = np.clip(u, -clamp, clamp)
         g = np.minimum(g, clamp)
-    return g / (1.0 + np.exp(-g)) * u
+    with np.errstate(over="ignore"):  # exp(-g) -> inf for very negative g gives silu(g) -> -0
+        return g / (1.0 + np.exp(-g)) * u
 
 
 def moe_forward_f64(layer, x, ids, wts, quantize):
