@@ -60,3 +60,22 @@ def test_product_binding_does_not_import_the_oracle():
             if f.endswith((".py", ".hip", ".h", ".cpp")):
                 text = open(os.path.join(root, f)).read()
                 assert "import oracle" not in text and "moe_oracle" not in text, f
+
+
+def test_header_is_c99_and_links(tmp_path):
+    """include/moe_block.h is a C header: a C99 program (-pedantic -Werror)
+    includes it, links against the library and sees the wire structs at the
+    protocol's sizes."""
+    src = tmp_path / "use.c"
+    src.write_text('#include "moe_block.h"\n#include <stdio.h>\n'
+                   "int main(void) {\n"
+                   "  moe_node n = {0}; moe_split s = {0}; moe_gguf_layer g = {0}; (void)s; (void)g;\n"
+                   "  printf(\"%zu %zu %zu %zu %d\\n\", sizeof(moe_wire_hello_request), sizeof(moe_wire_hello_response),\n"
+                   "         sizeof(moe_wire_request), sizeof(moe_wire_response), n.op);\n"
+                   "  return moe_status_str(MOE_ERR_FORMAT)[0] == 0;\n}\n")
+    exe = tmp_path / "use"
+    libdir = os.path.dirname(mb.LIB_PATH)
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Wextra", "-pedantic", "-Werror", "-I", os.path.join(REPO, "include"),
+                    str(src), "-o", str(exe), "-L", libdir, "-lmoe_block", f"-Wl,-rpath,{libdir}"], check=True)
+    r = subprocess.run([str(exe)], capture_output=True, text=True, check=True)
+    assert r.stdout.split() == ["24", "80", "40", "56", "0"]
