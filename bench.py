@@ -49,7 +49,12 @@ def parse():
     ap.add_argument("--layers", type=int, default=8, help="resident V3 layers the steps cycle over")
     ap.add_argument("--seed", type=int, default=2024)
     ap.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU-baseline sample budget (0 = skip)")
-    ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0 = min(16, cpus))")
+    ap.add_argument("--cpu-threads", type=int, default=0,
+                    help="CPU-baseline threads (0 = every CPU this job may use: the affinity mask capped by the "
+                         "cgroup quota)")
+    ap.add_argument("--trace-gaps", default="",
+                    help="only read a rocprofv3 kernel_trace.csv of a --workload c5 run and print the idle time "
+                         "between the graph replays' kernels per layer (the launch overhead), then exit")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the hipGraph")
     ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "boundary", "server"],
                     help="c2 (default): the headline V3 decode line; c1/c3/c4/c5: one line per measured case of "
@@ -122,11 +127,43 @@ def cpu_baseline(seconds: float, threads: int, seed: int):
         i += 1
     med = float(np.median(times)) * 1e6
     touched = (sh.n_used + 1) * sh.expert_bytes
-    log(f"cpu baseline: {len(times)} tokens, median {med:.0f} us/token, {touched / med / 1e3:.1f} GB/s")
+    hc = host_cpus()
+    log(f"cpu baseline: {len(times)} tokens, median {med:.0f} us/token, {touched / med / 1e3:.1f} GB/s on "
+        f"{threads} threads ({hc})")
     return {"value": round(med, 1), "unit": "us/token", "cores": threads, "kind": "port",
             "sample": f"{len(times)} V3 decode tokens (T=1, top-8 + shared, {n_tok} independent routings), "
                       f"oracle/libmoe_oracle.so on {threads} threads, median per token",
-            "gbps": round(touched / med / 1e3, 2)}
+            "gbps": round(touched / med / 1e3, 2), "cpu_model": hc["model"], "cpus_visible": hc["visible"],
+            "cpus_affinity": hc["affinity"], "cpu_quota": hc["quota"]}
+
+
+def host_cpus():
+    """The host's CPUs as this process sees them: the model name
+    (/proc/cpuinfo), os.cpu_count(), the affinity mask, the cgroup CPU quota
+    (cpu.max, None when unlimited), and `usable` = the affinity count capped
+    by the quota: the threads the job can run at once."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    visible = os.cpu_count() or 1
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        affinity = visible
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = float(q) / float(period)
+    except (OSError, ValueError):
+        pass
+    usable = affinity if quota is None else max(1, min(affinity, int(quota)))
+    return {"model": model, "visible": visible, "affinity": affinity, "quota": quota, "usable": usable}
 
 MFMA_FP4_PEAK_TFLOPS = 10100.0  # MI355X dense MXFP4 MFMA, vendor figure
 
@@ -178,7 +215,7 @@ def bench_config(args):
         step_bytes = float(sum(sh.touched_bytes(ids_np[i:i + 1]) for i in range(NL)))
         g = blk.graph_capture(list(range(NL)), [x[i:i + 1] for i in range(NL)], [ids[i:i + 1] for i in range(NL)],
                               [wts[i:i + 1] for i in range(NL)], [out[i:i + 1] for i in range(NL)])
-        for _ in range(max(1, args.warmup // 8)):
+        for _ in range(max(1, args.warmup // 8)):  # the first of these carries the graph's one-time set-up
             g.launch()
         torch.cuda.synchronize()
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -212,8 +249,12 @@ def bench_config(args):
                                    f"independent top-8 routing per layer, one hipGraph of {NL} layer calls "
                                    f"replayed {steps} times"},
             "us_per_layer": round(us_step / NL, 3),
-            "kernel_us_per_layer": round(kern_us_layer, 3),
-            "launch_overhead_us_per_layer": round(us_step / NL - kern_us_layer, 3),
+            # eager launches timed by HIP events around each kernel: an upper
+            # bound of the kernel time (the events add their own overhead)
+            "eager_event_kernel_us_per_layer": round(kern_us_layer, 3),
+            # idle time between the graph's kernels comes from a kernel trace of
+            # this run (rocprofv3 --kernel-trace, then bench.py --trace-gaps)
+            "launch_overhead_us_per_layer": None,
             "hbm_gbps": round(gbps, 1), "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
             "algorithmic_bytes_per_step": round(step_bytes),
             "tokens_per_s": round(1e6 / us_step, 1),
@@ -259,6 +300,10 @@ def bench_config(args):
         if gw is not None:
             gw.launch()
         torch.cuda.synchronize()
+        t_f = time.perf_counter()
+        gk.launch()  # first replay, untimed: one-time graph set-up stays out of the timed region
+        torch.cuda.synchronize()
+        first_replay = time.perf_counter() - t_f
         t_a = time.perf_counter()
         gk.launch()
         torch.cuda.synchronize()
@@ -295,6 +340,7 @@ def bench_config(args):
             "useful_tflops": round(tflops, 2),
             "mfma_frac_of_fp4_peak": round(tflops / MFMA_FP4_PEAK_TFLOPS, 5),
             "kernel_avg_us": avg,
+            "first_replay_us_untimed": round(first_replay * 1e6, 1),
         }
         log(f"{label}: {us_step:.1f} us/step, {gbps:.0f} GB/s ({gbps / HBM_PEAK_GBPS:.1%}), "
             f"{distinct[W:n].mean():.1f} distinct experts, kernels {avg}")
@@ -548,8 +594,51 @@ def bench_server(args):
     print(json.dumps(line), flush=True)
 
 
+def trace_gaps(path: str, n_layers: int = 40):
+    """Launch overhead of the C5 graph from a rocprofv3 kernel trace of a
+    `--workload c5` run: the longest run of back-to-back expert kernels
+    (k_gate_up*/k_down*, each starting within 100 us of the previous one's
+    end) is the timed replays; per layer = the idle time between consecutive
+    kernels of that run, max(0, start - previous end) summed, divided by the
+    layer calls in it (kernels / 2).  Also prints the run's span and summed
+    kernel time per layer."""
+    import csv
+
+    recs = []
+    with open(path, newline="") as f:
+        for r in csv.DictReader(f):
+            name = r["Kernel_Name"]
+            if name.startswith("k_gate_up") or name.startswith("k_down"):
+                recs.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name))
+    recs.sort()
+    if not recs:
+        raise SystemExit(f"bench: no expert kernels in {path}")
+    best, cur = (0, 0), 0
+    for i in range(1, len(recs) + 1):
+        if i == len(recs) or recs[i][0] - recs[i - 1][1] > 100_000:
+            if i - cur > best[1] - best[0]:
+                best = (cur, i)
+            cur = i
+    run = recs[best[0]:best[1]]
+    calls = len(run) / 2
+    gaps = sum(max(0, run[i][0] - run[i - 1][1]) for i in range(1, len(run))) / 1e3
+    busy = sum(e - b for b, e, _ in run) / 1e3
+    span = (run[-1][1] - run[0][0]) / 1e3
+    line = {
+        "metric": "C5 launch overhead per layer call (idle time between the graph's kernels, from a kernel trace)",
+        "value": round(gaps / calls, 3), "unit": "us/layer", "higher_is_better": False,
+        "layer_calls": int(calls), "steps": round(calls / n_layers, 2),
+        "span_us_per_layer": round(span / calls, 3), "kernel_us_per_layer": round(busy / calls, 3),
+        "trace": os.path.relpath(path, REPO) if os.path.isabs(path) else path,
+    }
+    print(json.dumps(line), flush=True)
+
+
 def main():
     args = parse()
+    if args.trace_gaps:
+        trace_gaps(args.trace_gaps)
+        return
     if args.copy_mib > 0:
         copy_calibration(args.copy_mib)
         return
@@ -611,6 +700,7 @@ def main():
         for i in range(lo, hi):
             blk.forward(layer_of[i], x[i:i + 1], ids[i:i + 1], wts[i:i + 1], out[i:i + 1])
 
+    first_replay = events_ms = None
     if args.eager:
         run_eager(0, W)
         torch.cuda.synchronize()
@@ -625,6 +715,13 @@ def main():
         if gw is not None:
             gw.launch()
         torch.cuda.synchronize()
+        # the first replay of a graph carries one-time set-up; replay the timed
+        # graph once untimed (same inputs, same outputs) so that the timed
+        # region is steady state whatever --steps is
+        t_f = time.perf_counter()
+        gk.launch()
+        torch.cuda.synchronize()
+        first_replay = time.perf_counter() - t_f
         ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         t_a = time.perf_counter()
         ev0.record(stream)
@@ -632,7 +729,9 @@ def main():
         ev1.record(stream)
         torch.cuda.synchronize()
         elapsed = time.perf_counter() - t_a
-        log(f"graph replay: wall {elapsed * 1e3:.3f} ms, events {ev0.elapsed_time(ev1):.3f} ms for {K} steps")
+        events_ms = ev0.elapsed_time(ev1)
+        log(f"graph replay: wall {elapsed * 1e3:.3f} ms, events {events_ms:.3f} ms for {K} steps "
+            f"(first, untimed replay {first_replay * 1e3:.3f} ms)")
         mode = "hipGraph"
     out_graph = out[W:n].clone()
 
@@ -672,7 +771,7 @@ def main():
 
     cpu = None
     if args.cpu_seconds > 0:
-        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        threads = args.cpu_threads or host_cpus()["usable"]
         cpu = cpu_baseline(args.cpu_seconds, threads, args.seed)
 
     res = {
@@ -701,6 +800,9 @@ def main():
         "hbm_frac": round(gbps / HBM_PEAK_GBPS, 4),
         "algorithmic_bytes_per_step": round(bytes_timed / K),
         "us_per_step_eager": round(eager_elapsed / K * 1e6, 3),
+        "us_per_step_events": round(events_ms * 1e3 / K, 3) if events_ms is not None else None,
+        "first_replay_us_untimed": round(first_replay * 1e6, 1) if first_replay is not None else None,
+        "kernel_sum_us": round(kernel_sum_us, 3),
         "kernel_avg_us": {k: round(v, 3) for k, v in avg.items()},
         "roofline": {
             "kernel": dominant,

@@ -192,6 +192,8 @@ enum {
 };
 #define MOE_GLU_SWIGLU 2
 #define MOE_GGML_F32 0
+#define MOE_GGML_F16 1
+#define MOE_GGML_BF16 30
 #define MOE_GGML_I32 26
 #define MOE_GGML_MXFP4 39
 
@@ -326,12 +328,16 @@ moe_status moe_server_handle(moe_server *srv, const void *msg, size_t len, void 
 moe_status moe_server_listen(moe_server *srv, const char *host, int port, int *bound_port);
 moe_status moe_server_serve(moe_server *srv, int max_connections);
 
-/* Router logits on the device: logits [T][E] = x [T][H] . W [E][H]^T in f32
- * (ggml_mul_mat(ffn_gate_inp, x), nano-glm/lib/models/glm_dsa/moe_block.h:52),
- * H % 4 == 0, pointers 16-byte aligned.  The router of moe_server_*; feeds
- * moe_route / moe_route_forward. */
+/* Router logits on the device: logits [T][E] = x [T][H] . W [E][H]^T with
+ * f32 accumulation (ggml_mul_mat(ffn_gate_inp, x),
+ * nano-glm/lib/models/glm_dsa/moe_block.h:52), H % 4 == 0, pointers 16-byte
+ * aligned.  W is f32 on the device; w_type is the ggml type it was widened
+ * from (MOE_GGML_F32, MOE_GGML_F16 or MOE_GGML_BF16): for f16 and bf16, x is
+ * rounded to that type before the products, as ggml-cpu's mul_mat converts
+ * src1 to src0's vec_dot_type.  The router of moe_server_*; feeds moe_route
+ * / moe_route_forward. */
 moe_status moe_router_logits(moe_ctx *ctx, const float *w_dev, const float *x_dev, int T, int E, int H,
-                             float *logits_dev, void *stream);
+                             int w_type, float *logits_dev, void *stream);
 
 /* Free a layer's device memory and return its bytes to the budget
  * (moe_tp_free, moe_tp.h:356-390). */
@@ -394,11 +400,24 @@ moe_status moe_route_forward(moe_ctx *ctx, int layer, const float *x_dev,
  * inputs x/ids/wts/out device pointers per layer) into one hipGraph.  The
  * reference pre-records one command buffer per (layer, die) and replays it
  * (moe_tp.h:646-701); this is the gfx950 counterpart, for a whole stack.
- * Needs moe_ctx_reserve for T beforehand (no allocation under capture). */
+ * Needs moe_ctx_reserve for T beforehand (no allocation under capture).
+ *
+ * A graph replays raw device pointers: the context's per-call scratch and
+ * the weights of the layers it captured.  While a graph is alive (captured
+ * and not yet destroyed) the context therefore refuses, with
+ * MOE_ERR_INVALID_ARG and nothing launched, every call that would move or
+ * free them: a moe_forward / moe_forward_host / moe_split_compute /
+ * moe_ctx_reserve that needs a larger scratch than the one reserved, and a
+ * moe_layer_release of a captured layer.  Reserve for the largest call
+ * first, and destroy the graphs before releasing their layers.  The
+ * caller's x/ids/wts/out buffers stay the caller's to keep alive. */
 moe_status moe_graph_capture(moe_ctx *ctx, int n_layers, const int *layers,
                              const float *const *x_dev, const int32_t *const *ids_dev,
                              const float *const *wts_dev, float *const *out_dev,
                              int T, uint32_t flags, moe_graph **out);
+/* MOE_ERR_INVALID_ARG for a graph whose context was destroyed (the
+ * graph's executable goes with the context; the handle stays valid for
+ * moe_graph_destroy). */
 moe_status moe_graph_launch(moe_graph *g, void *stream);
 void moe_graph_destroy(moe_graph *g);
 

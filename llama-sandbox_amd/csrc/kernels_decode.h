@@ -120,6 +120,23 @@ __global__ __launch_bounds__(256) void k_route(const float *__restrict__ logits,
 // tokens: each lane accumulates a strided quarter-row slice with FMAs, then
 // wave_sum.  grid (ceil(E/4), ceil(T/4)), 256 threads; H % 4 == 0, rows
 // 16-byte aligned.
+// x rounded to the router weight's type before the products (XR: 0 f32 = as
+// is, 1 f16, 2 bf16, each round to nearest even): ggml-cpu's mul_mat converts
+// src1 to src0's vec_dot_type (f16 -> f16, bf16 -> bf16) and accumulates the
+// products in f32.  A product of two f16 (or two bf16) values is exact in
+// f32, so only the order of the f32 sum differs from ggml's.
+template <int XR>
+__device__ __forceinline__ float router_x(float v) {
+  if (XR == 1) return (float)(_Float16)v;
+  if (XR == 2) {
+    const uint32_t u = __builtin_bit_cast(uint32_t, v);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return v;  // NaN stays NaN
+    return __builtin_bit_cast(float, (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u);
+  }
+  return v;
+}
+
+template <int XR>
 __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__ W, const float *__restrict__ x,
                                                        int T, int E, int H, float *__restrict__ logits) {
   const int lane = threadIdx.x & 63;
@@ -133,7 +150,8 @@ __global__ __launch_bounds__(256) void k_router_logits(const float *__restrict__
     for (int j = 0; j < 4; j++) {
       if (t0 + j >= T) break;
       const float4 v = reinterpret_cast<const float4 *>(x + (size_t)(t0 + j) * H)[i];
-      acc[j] = fmaf(w.x, v.x, fmaf(w.y, v.y, fmaf(w.z, v.z, fmaf(w.w, v.w, acc[j]))));
+      acc[j] = fmaf(w.x, router_x<XR>(v.x),
+                    fmaf(w.y, router_x<XR>(v.y), fmaf(w.z, router_x<XR>(v.z), fmaf(w.w, router_x<XR>(v.w), acc[j]))));
     }
   }
 #pragma unroll

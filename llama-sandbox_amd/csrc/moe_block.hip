@@ -22,6 +22,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <set>
 #include <string>
 #include <vector>
 
@@ -42,9 +43,10 @@ struct dev_layer {
   int n_mats = 0;      // E + has_shared (the shared expert is expert index E)
   dev_mat m[3];        // gate, up, down
   uint64_t bytes = 0;
+  int graph_refs = 0;  // live graphs (moe_graph_capture) that read these weights
 };
 
-struct scratch {
+struct work_bufs {
   // sized for (T, H, F, E, k)
   int T = 0, H = 0, F = 0, E = 0, k = 0;
   uint32_t *hq = nullptr; float *hd = nullptr;     // staged h: [P+T][F/32][16] dwords, [P+T][F/32]
@@ -64,6 +66,7 @@ struct scratch {
   size_t out_cap = 0;
   size_t h_rows = 0;     // rows written to htap by the last forward
   int last_F = 0;
+  bool timed = true;     // kernels on these buffers are timed by the profiler (moe_prof_*)
 };
 
 }  // namespace
@@ -90,7 +93,7 @@ struct moe_ctx {
   int n_cu = 256;
   uint64_t budget = 0, used = 0;
   std::map<int, dev_layer> layers;
-  scratch sc;
+  work_bufs sc;
   std::string err;
   int inject = 0;  // bit 0: forward fails, bit 1: budget forced to 0
   bool capturing = false;
@@ -99,6 +102,10 @@ struct moe_ctx {
   // moe_forward_host's pinned staging (x, ids, wts in; out back), grown on demand
   uint8_t *pin = nullptr;
   size_t pin_bytes = 0;
+  // Live graphs.  A graph holds raw device pointers to the scratch and to the
+  // weights of the layers it captured, so while one is alive the scratch is
+  // never reallocated and those layers are never released.
+  std::set<moe_graph *> graphs;
 };
 
 // HIP-event pair around one kernel launch while profiling is on (never
@@ -118,8 +125,8 @@ struct prof_scope {
     }
     return e;
   }
-  prof_scope(moe_ctx *ctx, int k, hipStream_t s) : c(ctx), kid(k), st(s) {
-    if (!c->prof.on || c->capturing) return;
+  prof_scope(moe_ctx *ctx, int k, hipStream_t s, bool timed) : c(ctx), kid(k), st(s) {
+    if (!timed || !c->prof.on || c->capturing) return;
     a = take(c->prof);
     b = a ? take(c->prof) : nullptr;
     if (a && b && hipEventRecord(a, st) != hipSuccess) {
@@ -143,10 +150,27 @@ struct prof_scope {
 };
 
 struct moe_graph {
-  moe_ctx *ctx = nullptr;
+  moe_ctx *ctx = nullptr;      // null once the context is destroyed
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
+  std::vector<int> layers;     // distinct layers the graph reads (one graph_refs count each)
 };
+
+// Drop a graph's executable and its holds on the context (its layers'
+// graph_refs and its entry in ctx->graphs).
+static void graph_detach(moe_graph *g) {
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  g->exec = nullptr;
+  g->graph = nullptr;
+  if (!g->ctx) return;
+  for (int l : g->layers) {
+    auto it = g->ctx->layers.find(l);
+    if (it != g->ctx->layers.end() && it->second.graph_refs > 0) it->second.graph_refs--;
+  }
+  g->ctx->graphs.erase(g);
+  g->ctx = nullptr;
+}
 
 // ---------------------------------------------------------------------------
 static moe_status fail(moe_ctx *c, moe_status s, const char *fmt, ...) {
@@ -198,17 +222,22 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 // ---------------------------------------------------------------------------
 // scratch
 
-static void scratch_free(scratch &s) {
+static void scratch_free(work_bufs &s) {
   void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.part, s.tick, s.grp, s.ids_in, s.out_buf};
   for (void *p : ptrs)
     if (p) (void)hipFree(p);
-  s = scratch();
+  s = work_bufs();
 }
 
 static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k) {
-  scratch &s = c->sc;
+  work_bufs &s = c->sc;
   if (s.hq && T <= s.T && H <= s.H && F <= s.F && E <= s.E && k <= s.k) return MOE_OK;
   if (c->capturing) return fail(c, MOE_ERR_INVALID_ARG, "scratch too small under graph capture; call moe_ctx_reserve first");
+  if (!c->graphs.empty())
+    return fail(c, MOE_ERR_INVALID_ARG,
+                "the per-call scratch would be reallocated while %zu captured graph(s) still point at it; destroy "
+                "them first, or reserve for the largest call before capturing",
+                c->graphs.size());
   T = T > s.T ? T : s.T;
   H = H > s.H ? H : s.H;
   F = F > s.F ? F : s.F;
@@ -273,6 +302,9 @@ extern "C" void moe_ctx_destroy(moe_ctx *c) {
   if (!c) return;
   (void)hipSetDevice(c->device);
   (void)hipDeviceSynchronize();
+  // graphs outlive the context only as empty handles: moe_graph_launch then
+  // refuses them and moe_graph_destroy frees the handle
+  while (!c->graphs.empty()) graph_detach(*c->graphs.begin());
   for (auto &kv : c->layers)
     for (dev_mat &m : kv.second.m)
       if (m.w) (void)hipFree(m.w);
@@ -558,7 +590,11 @@ extern "C" moe_status moe_layer_read_blocks(moe_ctx *c, int layer, int tensor, i
 
 extern "C" moe_status moe_layer_release(moe_ctx *c, int layer) {
   if (!c) return MOE_ERR_INVALID_ARG;
-  if (!c->layers.count(layer)) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layer);
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layer);
+  if (it->second.graph_refs > 0)
+    return fail(c, MOE_ERR_INVALID_ARG, "layer %d is read by %d captured graph(s); destroy them before releasing it",
+                layer, it->second.graph_refs);
   HIPC(c, hipSetDevice(c->device));
   HIPC(c, hipDeviceSynchronize());
   layer_drop(c, layer);
@@ -584,7 +620,7 @@ extern "C" moe_status moe_route(moe_ctx *c, const float *logits, const float *bi
     return fail(c, MOE_ERR_INVALID_ARG, "moe_route: bad arguments");
   HIPC(c, hipSetDevice(c->device));
   {
-    prof_scope ps(c, K_ROUTE, (hipStream_t)stream);
+    prof_scope ps(c, K_ROUTE, (hipStream_t)stream, true);
     hipLaunchKernelGGL(k_route, dim3(T), dim3(256), 0, (hipStream_t)stream, logits, bias, E, k, mode, norm,
                        scale, ids, wts);
   }
@@ -593,13 +629,19 @@ extern "C" moe_status moe_route(moe_ctx *c, const float *logits, const float *bi
 }
 
 extern "C" moe_status moe_router_logits(moe_ctx *c, const float *w, const float *x, int T, int E, int H,
-                                        float *logits, void *stream) {
+                                        int w_type, float *logits, void *stream) {
   if (!c) return MOE_ERR_INVALID_ARG;
-  if (!w || !x || !logits || T <= 0 || E <= 0 || H <= 0 || H % 4 || ((uintptr_t)w | (uintptr_t)x) % 16)
+  if (!w || !x || !logits || T <= 0 || E <= 0 || H <= 0 || H % 4 || ((uintptr_t)w | (uintptr_t)x) % 16 ||
+      (w_type != MOE_GGML_F32 && w_type != MOE_GGML_F16 && w_type != MOE_GGML_BF16))
     return fail(c, MOE_ERR_INVALID_ARG, "moe_router_logits: bad arguments");
   HIPC(c, hipSetDevice(c->device));
-  hipLaunchKernelGGL(k_router_logits, dim3(ceil_div(E, 4), ceil_div(T, 4)), dim3(256), 0, (hipStream_t)stream, w, x,
-                     T, E, H, logits);
+  const dim3 grid(ceil_div(E, 4), ceil_div(T, 4));
+  if (w_type == MOE_GGML_F16)
+    hipLaunchKernelGGL(k_router_logits<1>, grid, dim3(256), 0, (hipStream_t)stream, w, x, T, E, H, logits);
+  else if (w_type == MOE_GGML_BF16)
+    hipLaunchKernelGGL(k_router_logits<2>, grid, dim3(256), 0, (hipStream_t)stream, w, x, T, E, H, logits);
+  else
+    hipLaunchKernelGGL(k_router_logits<0>, grid, dim3(256), 0, (hipStream_t)stream, w, x, T, E, H, logits);
   HIPC(c, hipGetLastError());
   return MOE_OK;
 }
@@ -612,7 +654,7 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
     return fail(c, MOE_ERR_INVALID_ARG, "moe_group: bad arguments");
   HIPC(c, hipSetDevice(c->device));
   {
-    prof_scope ps(c, K_GROUP, (hipStream_t)stream);
+    prof_scope ps(c, K_GROUP, (hipStream_t)stream, true);
     hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, T, 0, 1, counts,
                        offsets, perm, inv, (int32_t *)nullptr, (const float *)nullptr, 0, (uint32_t *)nullptr,
                        (float *)nullptr, 0, (int32_t *)nullptr);
@@ -631,26 +673,26 @@ static void launch_gate_up_decode(dim3 g, hipStream_t st, const dev_layer &L, co
                      htap);
 }
 
-static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
-                                  int T, float *out, uint32_t flags, hipStream_t st);
+static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const float *x, const int32_t *ids,
+                                  const float *wts, int T, float *out, uint32_t flags, hipStream_t st);
 
 // The decode chain for T == 1, two launches: gate/up per (32-row unit, slot)
 // with SwiGLU and Q8_0 of h, then down per 16-row tile of H with one wave per
-// slot, the router weights and the slot-order combine.
-static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
-                                 float *out, uint32_t flags, hipStream_t st) {
+// slot, the router weights and the slot-order combine.  s: the per-call
+// buffers (the context's own, or the no-allocation entry point's).
+static moe_status forward_decode(moe_ctx *c, dev_layer &L, work_bufs &s, const float *x, const int32_t *ids,
+                                 const float *wts, float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
   const int k = d.n_used, E = d.n_expert, H = d.hidden, F = d.ffn;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
   const int shared = (d.has_shared && !per_slot && !(flags & MOE_FWD_NO_SHARED)) ? 1 : 0;
   const int S = k + shared;
-  scratch &s = c->sc;
   float *htap = c->taps ? s.htap : nullptr;
   const size_t lds1 = gate_up_lds_bytes(H, 1), lds2 = down_dec_lds_bytes(F, S);
   if (S > 16 || lds1 > 65536 || lds2 > 65536)
-    return forward_grouped(c, L, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
+    return forward_grouped(c, L, s, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
   {
-    prof_scope pg(c, K_GU_DECODE, st);
+    prof_scope pg(c, K_GU_DECODE, st, s.timed);
     // the balanced kernels run one workgroup per CU: for shapes too small to
     // fill half of the CUs that way (C1), the (unit, slot) grid spreads wider
     const long n_tasks = (long)S * (F / MOE_UNIT) * 4;
@@ -674,7 +716,7 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
   s.h_rows = htap ? (size_t)S : 0;
   s.last_F = F;
   {
-    prof_scope pd(c, K_DOWN_DECODE, st);
+    prof_scope pd(c, K_DOWN_DECODE, st, s.timed);
     hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].w, s.hq, s.hd, ids,
                        wts, k, E, S, F, H, per_slot ? 1 : 0, out);
   }
@@ -687,8 +729,8 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, const float *x, const
 // MFMA above that (items of at most 8 rows).
 static bool use_octets(int T) { return T > 4; }
 
-static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, const int32_t *ids, const float *wts,
-                                  int T, float *out, uint32_t flags, hipStream_t st) {
+static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const float *x, const int32_t *ids,
+                                  const float *wts, int T, float *out, uint32_t flags, hipStream_t st) {
   const moe_layer_desc &d = L.d;
   const int k = d.n_used, E = d.n_expert, P = T * k, H = d.hidden, F = d.ffn;
   const bool per_slot = flags & MOE_FWD_PER_SLOT;
@@ -698,7 +740,6 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
                 MOE_GROUP_MAX_E);
   const bool oct = use_octets(T);
   const int BT = oct ? 8 : 4;
-  scratch &s = c->sc;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
   // octets: gate/up on items of up to 16 rows (two octets per wave) where the
   // shape has an instance and the batch averages 2 pairs per expert or more
@@ -710,14 +751,14 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
   {
-    prof_scope pgr(c, K_GROUP, st);
+    prof_scope pgr(c, K_GROUP, st, s.timed);
     hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
                        shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, 16,
                        o2 ? items16 : (int32_t *)nullptr);
   }
   const int cap = group_item_cap(T, k, E, BT);
   {
-    prof_scope pg(c, K_GU_GROUPED, st);
+    prof_scope pg(c, K_GU_GROUPED, st, s.timed);
 #define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
 #define MOE_GU_ARGS16 L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items16, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
     const dim3 g16(F / (2 * MOE_UNIT), group_item_cap(T, k, E, 16));
@@ -732,7 +773,7 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
   s.h_rows = htap ? (size_t)P + (shared ? T : 0) : 0;
   s.last_F = F;
   {
-    prof_scope pd(c, K_DOWN_GROUPED, st);
+    prof_scope pd(c, K_DOWN_GROUPED, st, s.timed);
 #define MOE_DN_ARGS L.m[T_DOWN].w, s.hq, s.hd, P + T, items, perm, wts, F, H, s.y
     const dim3 gdo(H / 128, cap);
     const size_t lo = octet_lds_bytes(F / MOE_QK);
@@ -746,7 +787,7 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, const float *x, cons
 #undef MOE_DN_ARGS
   }
   {
-    prof_scope pc(c, K_COMBINE, st);
+    prof_scope pc(c, K_COMBINE, st, s.timed);
     if ((reinterpret_cast<uintptr_t>(out) & 15) == 0)  // float4 stores
       hipLaunchKernelGGL(k_combine4, dim3(ceil_div((long)T * (H / 4), 256)), dim3(256), 0, st, s.y, inv, T, k, H,
                          shared, per_slot ? 1 : 0, out);
@@ -769,8 +810,8 @@ extern "C" moe_status moe_forward(moe_ctx *c, int layer, const float *x, const i
   if (!c->capturing) HIPC(c, hipSetDevice(c->device));
   moe_status st = scratch_reserve(c, T, L.d.hidden, L.d.ffn, L.d.n_expert, L.d.n_used);
   if (st != MOE_OK) return st;
-  if (T == 1) return forward_decode(c, L, x, ids, wts, out, flags, (hipStream_t)stream);
-  return forward_grouped(c, L, x, ids, wts, T, out, flags, (hipStream_t)stream);
+  if (T == 1) return forward_decode(c, L, c->sc, x, ids, wts, out, flags, (hipStream_t)stream);
+  return forward_grouped(c, L, c->sc, x, ids, wts, T, out, flags, (hipStream_t)stream);
 }
 
 extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, const int32_t *ids,
@@ -783,7 +824,7 @@ extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, co
   HIPC(c, hipSetDevice(c->device));
   moe_status st = scratch_reserve(c, T, d.hidden, d.ffn, d.n_expert, d.n_used);
   if (st != MOE_OK) return st;
-  scratch &s = c->sc;
+  work_bufs &s = c->sc;
   const size_t P = (size_t)T * d.n_used;
   const size_t n_out = (flags & MOE_FWD_PER_SLOT) ? P * d.hidden : (size_t)T * d.hidden;
   // the caller's buffers are pageable: stage them through one pinned buffer in
@@ -840,7 +881,7 @@ extern "C" moe_status moe_graph_capture(moe_ctx *c, int n_layers, const int *lay
     auto it = c->layers.find(layers[i]);
     if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident", layers[i]);
     const moe_layer_desc &d = it->second.d;
-    const scratch &s = c->sc;
+    const work_bufs &s = c->sc;
     if (!s.hq || T > s.T || d.hidden > s.H || d.ffn > s.F || d.n_expert > s.E || d.n_used > s.k)
       return fail(c, MOE_ERR_INVALID_ARG, "moe_graph_capture: call moe_ctx_reserve for this shape first");
   }
@@ -874,20 +915,23 @@ extern "C" moe_status moe_graph_capture(moe_ctx *c, int n_layers, const int *lay
   mg->ctx = c;
   mg->graph = graph;
   mg->exec = exec;
+  std::set<int> distinct(layers, layers + n_layers);
+  mg->layers.assign(distinct.begin(), distinct.end());
+  for (int l : mg->layers) c->layers[l].graph_refs++;
+  c->graphs.insert(mg);
   *g = mg;
   return MOE_OK;
 }
 
 extern "C" moe_status moe_graph_launch(moe_graph *g, void *stream) {
-  if (!g) return MOE_ERR_INVALID_ARG;
+  if (!g || !g->ctx || !g->exec) return MOE_ERR_INVALID_ARG;  // a graph whose context was destroyed
   HIPC(g->ctx, hipGraphLaunch(g->exec, (hipStream_t)stream));
   return MOE_OK;
 }
 
 extern "C" void moe_graph_destroy(moe_graph *g) {
   if (!g) return;
-  if (g->exec) (void)hipGraphExecDestroy(g->exec);
-  if (g->graph) (void)hipGraphDestroy(g->graph);
+  graph_detach(g);
   delete g;
 }
 

@@ -26,7 +26,8 @@ struct srv_layer {
   bool served = false;  // a MoE layer with MXFP4 experts and a learned router
   int route_mode = MOE_ROUTE_SIGMOID, route_norm = 0;
   float route_scale = 1.0f;
-  float *w = nullptr;     // router [E][H] f32
+  float *w = nullptr;     // router [E][H] f32 (widened exactly from the file's f32 / f16 / bf16)
+  int w_type = MOE_GGML_F32;  // the file's ggml type of the router (x is rounded to it)
   float *bias = nullptr;  // [E] f32 or null
 };
 
@@ -168,6 +169,7 @@ static moe_status server_open(moe_server *s, const char *path, uint64_t budget) 
                                            (M.err.empty() ? std::string("missing or not [n_embd, n_expert]") : M.err));
     }
     L.w = srv_upload(w);
+    L.w_type = tw->type;
     if (tb) L.bias = srv_upload(bias);
     if (!L.w || (tb && !L.bias)) {
       return srv_fail(s, MOE_ERR_HIP, "router upload failed");
@@ -289,7 +291,7 @@ static bool srv_eval(moe_server *s, const moe_wire_request &rq, const void *x, u
   if (ok && x != s->pin_x) memcpy(s->pin_x, x, n * 4);
   ok = ok && hipEventRecord(s->ev[0], s->stream) == hipSuccess &&
        hipMemcpyAsync(s->x, s->pin_x, n * 4, hipMemcpyHostToDevice, s->stream) == hipSuccess &&
-       moe_router_logits(s->ctx, L.w, s->x, T, E, H, s->logits, s->stream) == MOE_OK &&
+       moe_router_logits(s->ctx, L.w, s->x, T, E, H, L.w_type, s->logits, s->stream) == MOE_OK &&
        moe_route(s->ctx, s->logits, L.bias, T, E, k, L.route_mode, L.route_norm, L.route_scale, s->ids, s->wts,
                  s->stream) == MOE_OK &&
        hipEventRecord(s->ev[1], s->stream) == hipSuccess &&

@@ -37,7 +37,8 @@ T_GATE, T_UP, T_DOWN = 0, 1, 2
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_last_error", "moe_status_str", "moe_ctx_budget_left",
     "moe_ctx_reserve", "moe_layer_upload", "moe_layer_generate", "moe_layer_read_blocks",
-    "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward", "moe_forward_host",
+    "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward",
+    "moe_forward_host",
     "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
     "moe_prof_enable", "moe_prof_read", "moe_debug_set_taps",
     "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
@@ -50,7 +51,7 @@ EXPORTS = (
 (NODE_NONE, NODE_RESHAPE, NODE_VIEW, NODE_PERMUTE, NODE_TRANSPOSE, NODE_MUL_MAT_ID, NODE_CLAMP, NODE_MUL, NODE_GLU,
  NODE_ADD, NODE_OTHER) = range(11)
 GLU_SWIGLU = 2
-GGML_F32, GGML_I32, GGML_MXFP4 = 0, 26, 39
+GGML_F32, GGML_F16, GGML_BF16, GGML_I32, GGML_MXFP4 = 0, 1, 30, 26, 39
 
 # nano-glm moe-server protocol v2 (include/moe_block.h, moe_wire_*)
 WIRE_MAGIC, WIRE_VERSION = 0x454F4D4E, 2
@@ -224,7 +225,7 @@ def load_library(path: str | None = None):
     L.moe_split_compute.restype = st
     L.moe_split_compute.argtypes = [_vp, ctypes.POINTER(ctypes.POINTER(MoeNode)), ctypes.c_int]
     L.moe_router_logits.restype = st
-    L.moe_router_logits.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]
+    L.moe_router_logits.argtypes = [_vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp]
     if path is None:
         _lib = L
     return L
@@ -268,6 +269,60 @@ def read_gguf_layer(path: str, layer: int) -> GgufLayer:
 def _ptr(t) -> int | None:
     """Device pointer of a torch tensor (or None)."""
     return None if t is None else int(t.data_ptr())
+
+
+# ---- argument checks ---------------------------------------------------------------
+# The C-ABI takes raw pointers and sizes: a tensor of the wrong dtype, shape or
+# device would make the kernels read or write out of bounds.  Every wrapper
+# below checks its tensors before the call and raises ValueError instead.
+# The order (dtype, shape, contiguity, device) lets the CPU tests reach each
+# refusal with host tensors.
+
+def check_tensor(t, name: str, dtype: str, shape=None, device: bool = True):
+    """t: a torch tensor of `dtype` ("float32", "int32", ...), `shape` (a
+    tuple, None entries match anything), contiguous, on a GPU if `device`."""
+    if t is None or not hasattr(t, "data_ptr"):
+        raise ValueError(f"{name}: expected a torch tensor, got {type(t).__name__}")
+    if str(t.dtype) != f"torch.{dtype}":
+        raise ValueError(f"{name}: dtype {t.dtype}, expected torch.{dtype}")
+    if shape is not None:
+        if t.dim() != len(shape) or any(want is not None and got != want for got, want in zip(t.shape, shape)):
+            raise ValueError(f"{name}: shape {tuple(t.shape)}, expected {tuple(shape)}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name}: not contiguous")
+    if device and t.device.type != "cuda":
+        raise ValueError(f"{name}: on {t.device}, expected a ROCm device tensor")
+
+
+def check_forward_args(desc, x, ids, wts, out, flags: int = 0):
+    """moe_forward's tensors: x float32 [T, H]; ids int32 / wts float32
+    [T, k]; out float32 [T, H], or [T, k, H] with MOE_FWD_PER_SLOT.  desc:
+    the layer's LayerDesc (None: the layer is unknown here, the library
+    answers MOE_ERR_NOT_RESIDENT; only dtypes and layout are checked)."""
+    H = desc.hidden if desc is not None else None
+    k = desc.n_used if desc is not None else None
+    check_tensor(x, "x", "float32", (None, H), device=False)
+    T = int(x.shape[0])
+    if T <= 0:
+        raise ValueError("x: no tokens")
+    check_tensor(ids, "ids", "int32", (T, k), device=False)
+    check_tensor(wts, "wts", "float32", (T, k), device=False)
+    check_tensor(out, "out", "float32", (T, k, H) if flags & MOE_FWD_PER_SLOT else (T, H), device=False)
+    for t, nm in ((x, "x"), (ids, "ids"), (wts, "wts"), (out, "out")):
+        if t.device.type != "cuda":
+            raise ValueError(f"{nm}: on {t.device}, expected a ROCm device tensor")
+    return T
+
+
+def check_host_forward_args(desc, x, ids, wts):
+    """moe_forward_host's numpy arrays: x [T, H], ids / wts [T, k]."""
+    if x.ndim != 2 or x.shape[1] != desc.hidden or x.shape[0] <= 0:
+        raise ValueError(f"x: shape {x.shape}, expected (T, {desc.hidden})")
+    T = x.shape[0]
+    for a, nm in ((ids, "ids"), (wts, "wts")):
+        if a.shape != (T, desc.n_used):
+            raise ValueError(f"{nm}: shape {a.shape}, expected ({T}, {desc.n_used})")
+    return T
 
 
 def _stream(stream) -> int | None:
@@ -382,30 +437,51 @@ class MoeBlock:
 
     # -- per call (torch device tensors) ---------------------------------------
     def route(self, logits, k: int, mode: int, norm: bool, scale: float, ids, wts, bias=None, stream=None):
+        check_tensor(logits, "logits", "float32", (None, None))
         T, E = logits.shape
+        check_tensor(ids, "ids", "int32", (T, k))
+        check_tensor(wts, "wts", "float32", (T, k))
+        if bias is not None:
+            check_tensor(bias, "bias", "float32", (E,))
         self._check(self.lib.moe_route(self.h, _ptr(logits), _ptr(bias), T, E, k, mode, int(norm), scale,
                                        _ptr(ids), _ptr(wts), _stream(stream)), "moe_route")
 
-    def router_logits(self, w, x, logits, stream=None):
-        """logits [T][E] = x [T][H] . w [E][H]^T (f32 device tensors)."""
+    def router_logits(self, w, x, logits, w_type: int = 0, stream=None):
+        """logits [T][E] = x [T][H] . w [E][H]^T (f32 device tensors); w_type:
+        the ggml type w was widened from (GGML_F32 / GGML_F16 / GGML_BF16: x
+        is rounded to it first, as ggml-cpu's mul_mat does)."""
+        check_tensor(x, "x", "float32", (None, None))
         T, H = x.shape
+        check_tensor(w, "w", "float32", (None, H))
         E = w.shape[0]
-        self._check(self.lib.moe_router_logits(self.h, _ptr(w), _ptr(x), T, E, H, _ptr(logits), _stream(stream)),
+        check_tensor(logits, "logits", "float32", (T, E))
+        self._check(self.lib.moe_router_logits(self.h, _ptr(w), _ptr(x), T, E, H, w_type, _ptr(logits),
+                                               _stream(stream)),
                     "moe_router_logits")
 
     def group(self, ids, E: int, counts, offsets, perm, inv=None, stream=None):
+        check_tensor(ids, "ids", "int32", (None, None))
         T, k = ids.shape
+        check_tensor(counts, "counts", "int32", (E,))
+        check_tensor(offsets, "offsets", "int32", (E + 1,))
+        check_tensor(perm, "perm", "int32", (T * k,))
+        if inv is not None:
+            check_tensor(inv, "inv", "int32", (T * k,))
         self._check(self.lib.moe_group(self.h, _ptr(ids), T, k, E, _ptr(counts), _ptr(offsets), _ptr(perm),
                                        _ptr(inv), _stream(stream)), "moe_group")
 
     def forward(self, layer: int, x, ids, wts, out, flags: int = 0, stream=None):
-        T = x.shape[0]
+        T = check_forward_args(self.descs.get(layer), x, ids, wts, out, flags)
         self._check(self.lib.moe_forward(self.h, layer, _ptr(x), _ptr(ids), _ptr(wts), T, _ptr(out), flags,
                                          _stream(stream)), "moe_forward")
 
     def route_forward(self, layer: int, x, logits, ids, wts, out, mode: int, norm: bool = True,
                       scale: float = 1.0, bias=None, flags: int = 0, stream=None):
-        T = x.shape[0]
+        d = self.descs.get(layer)
+        T = check_forward_args(d, x, ids, wts, out, flags)
+        check_tensor(logits, "logits", "float32", (T, d.n_expert if d is not None else None))
+        if bias is not None:
+            check_tensor(bias, "bias", "float32", (logits.shape[1],))
         self._check(self.lib.moe_route_forward(self.h, layer, _ptr(x), _ptr(logits), _ptr(bias), T, mode,
                                                int(norm), scale, _ptr(ids), _ptr(wts), _ptr(out), flags,
                                                _stream(stream)), "moe_route_forward")
@@ -420,7 +496,7 @@ class MoeBlock:
         x = np.ascontiguousarray(x, np.float32)
         ids = np.ascontiguousarray(ids, np.int32)
         wts = np.ascontiguousarray(wts, np.float32)
-        T = x.shape[0]
+        T = check_host_forward_args(d, x, ids, wts)
         shape = (T, d.n_used, d.hidden) if flags & MOE_FWD_PER_SLOT else (T, d.hidden)
         out = np.empty(shape, np.float32)
         self._check(self.lib.moe_forward_host(self.h, layer, x.ctypes.data, ids.ctypes.data, wts.ctypes.data,
@@ -429,7 +505,12 @@ class MoeBlock:
 
     def graph_capture(self, layers, xs, ids, wts, outs, flags: int = 0) -> Graph:
         n = len(layers)
+        if n == 0 or not (len(xs) == len(ids) == len(wts) == len(outs) == n):
+            raise ValueError("graph_capture: one x/ids/wts/out per layer")
         T = xs[0].shape[0]
+        for i in range(n):
+            if check_forward_args(self.descs.get(layers[i]), xs[i], ids[i], wts[i], outs[i], flags) != T:
+                raise ValueError(f"graph_capture: layer {i} has {xs[i].shape[0]} tokens, expected {T}")
         la = (ctypes.c_int * n)(*layers)
         mk = lambda ts: (_vp * n)(*[_ptr(t) for t in ts])  # noqa: E731
         px, pi, pw, po = mk(xs), mk(ids), mk(wts), mk(outs)
@@ -454,10 +535,20 @@ class MoeBlock:
     def set_taps(self, on: bool = True):
         self._check(self.lib.moe_debug_set_taps(self.h, int(on)), "moe_debug_set_taps")
     def debug_quantize_q8_0(self, x, qs, d, stream=None):
+        check_tensor(x, "x", "float32")
+        n = x.numel()
+        check_tensor(qs, "qs", "int8", (n,) if qs.dim() == 1 else tuple(x.shape))
+        if d.numel() != n // 32 or d.element_size() != 2:
+            raise ValueError("d: expected n/32 16-bit scales")
+        check_tensor(d, "d", str(d.dtype).replace("torch.", ""))
         self._check(self.lib.moe_debug_quantize_q8_0(self.h, _ptr(x), x.numel(), _ptr(qs), _ptr(d),
                                                      _stream(stream)), "moe_debug_quantize_q8_0")
 
     def debug_wave_sum(self, x, out, stream=None):
+        check_tensor(x, "x", "float32")
+        if x.numel() % 64 or out.numel() < x.numel() // 64:
+            raise ValueError("debug_wave_sum: x of 64*n floats, out of n")
+        check_tensor(out, "out", "float32")
         self._check(self.lib.moe_debug_wave_sum(self.h, _ptr(x), x.numel() // 64, _ptr(out), _stream(stream)),
                     "moe_debug_wave_sum")
 

@@ -260,11 +260,12 @@ class OracleLayer:
         return res
 
     def forward_from_h(self, ids: np.ndarray, wts: np.ndarray, h: np.ndarray, h_shared=None,
-                       n_threads: int = 1) -> np.ndarray:
+                       n_threads: int = 1, per_slot: bool = False):
         """The block from a given SwiGLU output: h f32 [T, k, F] (and the
         shared expert's [T, F]) -> Q8_0(h) -> down x router weight ->
-        combine -> out f32 [T, H].  A test passes another implementation's
-        h here to reproduce its activation quantization exactly."""
+        combine -> out f32 [T, H] (per_slot: (out, the weighted per-slot rows
+        [T, k, H])).  A test passes another implementation's h here to
+        reproduce its activation quantization exactly."""
         ids = np.ascontiguousarray(ids, np.int32)
         wts = np.ascontiguousarray(wts, np.float32)
         T = ids.shape[0]
@@ -273,10 +274,11 @@ class OracleLayer:
             rows.append(np.asarray(h_shared, np.float32).reshape(T, self.F))
         hh = np.ascontiguousarray(np.concatenate(rows, axis=0), np.float32)
         out = np.empty((T, self.H), np.float32)
+        ps = np.empty((T, self.k, self.H), np.float32) if per_slot else None
         s, keep = self._struct()
         rc = lib().mo_moe_forward_from_h(ctypes.byref(s), T, _p(ids, _i32p), _p(wts, _f32p), _p(hh, _f32p),
-                                         _p(out, _f32p), None, int(n_threads))
+                                         _p(out, _f32p), None if ps is None else _p(ps, _f32p), int(n_threads))
         del keep
         if rc != 0:
             raise ValueError("oracle forward_from_h rejected its arguments")
-        return out
+        return (out, ps) if per_slot else out

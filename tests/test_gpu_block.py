@@ -12,105 +12,9 @@ import pytest
 
 import moe_block as mb
 import workloads as wl
+from parity import Taps, assert_rms_close, check_block, gpu_h, oracle_layer, run_block, say
 
 pytestmark = pytest.mark.gpu
-
-TOL = 1e-3  # max-abs error as a fraction of the oracle output's RMS
-
-
-def say(*a):
-    print("[gpu]", *a, flush=True)
-
-
-def rms(a):
-    return float(np.sqrt(np.mean(np.asarray(a, np.float64) ** 2)))
-
-
-def assert_rms_close(got, ref, tol=TOL, what=""):
-    """max|got - ref| <= tol * RMS(ref) over the finite outputs, and the same
-    outputs non-finite on both sides.  The synthetic weights (E8M0 up to 2^2,
-    codes up to 12) make |h| exceed 65504 * 127 for some tokens; Q8_0 stores
-    d = amax/127 as fp16 (ggml's block_q8_0), so d becomes inf and the down
-    rows of that slot inf/NaN, on the oracle exactly as in ggml-cpu."""
-    got = np.asarray(got, np.float64)
-    ref = np.asarray(ref, np.float64)
-    fin = np.isfinite(ref)
-    assert np.array_equal(np.isfinite(got), fin), f"{what}: non-finite outputs differ"
-    if not fin.any():
-        say(f"{what} all {ref.size} outputs non-finite on both sides")
-        return
-    r = rms(ref[fin])
-    err = float(np.max(np.abs(got[fin] - ref[fin])))
-    nf = int(ref.size - fin.sum())
-    say(f"{what} rms(ref)={r:.4e} max|diff|={err:.3e} ratio={err / r:.3e}" + (f" non-finite={nf}" if nf else ""))
-    assert err <= tol * r, f"{what}: max|diff| {err:.3e} > {tol} * rms {r:.3e}"
-
-
-class _Taps:
-    """Stands in for the block in check_block when the h taps were already
-    read (a subset of the tokens of a larger call)."""
-
-    def __init__(self, h, h_shared):
-        self.h, self.h_shared = h, h_shared
-
-
-def gpu_h(blk, oracle, shape, ids, shared=None):
-    """The GPU's SwiGLU output (pre-quantization) of the last forward, in the
-    oracle's row order: routed [T, k, F] (pair t*k+s) and shared [T, F] or
-    None.  Decode (T == 1) keeps one row per slot; the grouped chain keeps
-    grouped rows (pair p at row inv[p]) then the shared expert's T rows."""
-    if isinstance(blk, _Taps):
-        return blk.h, blk.h_shared
-    T, k = ids.shape
-    F, P = shape.ffn, T * k
-    has_sh = shape.has_shared if shared is None else shared
-    n = P + (T if has_sh else 0)
-    rows = blk.debug_last_h(n * F).reshape(n, F)
-    inv = np.arange(P) if T == 1 else oracle.group(ids, shape.n_expert)["inv"]
-    return rows[inv].reshape(T, k, F), (rows[P:P + T] if has_sh else None)
-
-
-def check_block(oracle, L, blk, shape, x, ids, wts, got, what, n_threads=16):
-    """Parity of one forward, in two stages.
-
-    1. gate/up + clamp + SwiGLU: the GPU's h against the oracle's h, max|dh|
-       <= 2e-4 * max|h| per row (only the f32 summation order differs; the
-       bound leaves room for cancellation in the gate/up sums, which is
-       large when the clamp is active).
-    2. The output, max|d| <= TOL * RMS: against the oracle run end to end
-       for every token whose Q8_0(h) codes come out identical on both sides,
-       and for a token where an h value sits so close to a Q8_0 rounding
-       boundary that the two f32 orders round it to neighbouring codes,
-       against the oracle's down path fed the GPU's h (the same Q8_0(h)
-       codes: the activation quantization reproduced).  The number of such
-       tokens is reported."""
-    ref = L.forward(x, ids, wts, n_threads=n_threads, taps=True)
-    hg, hgs = gpu_h(blk, oracle, shape, ids)
-    pairs = [(hg, ref["h"], "h")] + ([(hgs, ref["h_shared"], "h shared")] if hgs is not None else [])
-    for a, b, nm in pairs:
-        a2 = a.reshape(-1, a.shape[-1]).astype(np.float64)
-        b2 = b.reshape(-1, b.shape[-1]).astype(np.float64)
-        scale = np.maximum(np.abs(b2).max(axis=1, keepdims=True), 1e-30)
-        worst = float((np.abs(a2 - b2) / scale).max())
-        say(f"{what} {nm}: max|dh|/max|h| = {worst:.3e}")
-        assert worst <= 2e-4, f"{what} {nm}: max|dh|/max|h| = {worst:.3e}"
-    T = x.shape[0]
-    flips = []
-    for t in range(T):
-        codes_same = True
-        for a, b in [(hg[t], ref["h"][t])] + ([(hgs[t], ref["h_shared"][t])] if hgs is not None else []):
-            qa, da = oracle.quantize_q8_0(a)
-            qb, db = oracle.quantize_q8_0(b)
-            codes_same = codes_same and np.array_equal(qa, qb) and np.array_equal(da, db)
-        if codes_same:
-            assert_rms_close(got[t], ref["out"][t], what=f"{what} t{t}")
-        else:
-            flips.append(t)
-            same_q = L.forward_from_h(ids[t:t + 1], wts[t:t + 1], hg[t:t + 1],
-                                      None if hgs is None else hgs[t:t + 1], n_threads=n_threads)
-            assert_rms_close(got[t], same_q[0], what=f"{what} t{t} (same Q8_0(h) codes)")
-    say(f"{what}: {len(flips)} of {T} tokens with an h value on a Q8_0 rounding boundary", flips[:16])
-    return ref
 
 
 @pytest.fixture(scope="module")
@@ -126,25 +30,6 @@ def blk(torch_dev):
     b.set_taps(True)
     yield b
     b.close()
-
-
-def run_block(blk, torch_dev, layer, x, ids, wts, flags=0):
-    torch, dev = torch_dev
-    T = x.shape[0]
-    d = blk.descs[layer]
-    shape = (T, d.n_used, d.hidden) if flags & mb.MOE_FWD_PER_SLOT else (T, d.hidden)
-    out = torch.empty(shape, dtype=torch.float32, device=dev)
-    blk.forward(layer, torch.from_numpy(x).to(dev), torch.from_numpy(ids).to(dev),
-                torch.from_numpy(wts).to(dev), out, flags)
-    torch.cuda.synchronize()
-    return out.cpu().numpy()
-
-
-def oracle_layer(oracle, shape, seed, layer, ids, clamp=None, e_lo=124, e_span=7):
-    return oracle.OracleLayer.generated(seed, layer, shape.hidden, shape.ffn, shape.n_expert, shape.n_used,
-                                        experts=sorted(set(np.asarray(ids).ravel().tolist())),
-                                        shared=shape.has_shared,
-                                        clamp=shape.clamp if clamp is None else clamp, e_lo=e_lo, e_span=e_span)
 
 
 # ---- C1: small layer, decode ---------------------------------------------------------
@@ -173,9 +58,8 @@ def test_c1_decode_per_slot(blk, torch_dev, oracle, c1):
     ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
     say("C1 per-slot")
     got = run_block(blk, torch_dev, 1, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
-    ref = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts, per_slot=True)["per_slot"]
-    for s in range(c1.n_used):
-        assert_rms_close(got[0, s], ref[0, s], what=f"C1 slot {s}")
+    check_block(oracle, oracle_layer(oracle, c1, 101, 1, ids), blk, c1, x, ids, wts, got, "C1 per-slot",
+                per_slot=True)
 
 
 def test_c1_route_forward_end_to_end(blk, torch_dev, oracle, c1):
@@ -224,8 +108,8 @@ def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
     got = run_block(blk, torch_dev, 1, x, ids, wts)
     check_block(oracle, oracle_layer(oracle, c1, 101, 1, ids), blk, c1, x, ids, wts, got, "C1 grouped")
     ps = run_block(blk, torch_dev, 1, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
-    refps = oracle_layer(oracle, c1, 101, 1, ids).forward(x, ids, wts, per_slot=True)["per_slot"]
-    assert_rms_close(ps, refps, what="C1 grouped per-slot")
+    check_block(oracle, oracle_layer(oracle, c1, 101, 1, ids), blk, c1, x, ids, wts, ps, "C1 grouped per-slot",
+                per_slot=True)
 
 
 def test_c1_grouped_two_octets_per_wave(blk, torch_dev, oracle, c1):
@@ -301,25 +185,17 @@ def test_c2_decode(blk, torch_dev, oracle, v3, seed):
 def test_c2_decode_per_slot_and_no_shared(blk, torch_dev, oracle, v3):
     """V3 decode without the shared expert: 8 slots, so the gate/up work (2048
     tasks) is not 9 per workgroup and runs on k_gate_up_bal (every unit met
-    through a ticket) instead of k_gate_up_bal2.  Per-slot rows (the MUL
-    node) against the oracle's, and the slot sum without the shared expert
-    against the per-slot rows added in slot order on the host."""
+    through a ticket) instead of k_gate_up_bal2.  Every per-slot row (the
+    MUL node) against the oracle's, a row whose Q8_0(h) codes differ through
+    the oracle's down path on the GPU's h; and the slot sum without the
+    shared expert against the per-slot rows added in slot order on the
+    host."""
     x, lg = wl.make_inputs(v3, 1, 21)
     ids, wts = oracle.route(lg, v3.n_used, v3.route_mode, norm=True)
     say("C2 per-slot / no shared", ids.tolist())
     ps = run_block(blk, torch_dev, 2, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
-    L = oracle_layer(oracle, v3, 202, 2, ids)
-    ref = L.forward(x, ids, wts, per_slot=True, taps=True)
-    hg, _ = gpu_h(blk, oracle, v3, ids, shared=False)
-    worst = float((np.abs(hg.astype(np.float64) - ref["h"]) / np.maximum(np.abs(ref["h"]).max(axis=-1, keepdims=True),
-                                                                          1e-30)).max())
-    say(f"C2 per-slot h: max|dh|/max|h| = {worst:.3e}")
-    assert worst <= 2e-4
-    for s in range(v3.n_used):
-        qa, da = oracle.quantize_q8_0(hg[0, s])
-        qb, db = oracle.quantize_q8_0(ref["h"][0, s])
-        if np.array_equal(qa, qb) and np.array_equal(da, db):
-            assert_rms_close(ps[0, s], ref["per_slot"][0, s], what=f"C2 slot {s}")
+    check_block(oracle, oracle_layer(oracle, v3, 202, 2, ids), blk, v3, x, ids, wts, ps, "C2 per-slot",
+                per_slot=True)
     ns = run_block(blk, torch_dev, 2, x, ids, wts, flags=mb.MOE_FWD_NO_SHARED)
     acc = ps[0, 0].copy()
     for s in range(1, v3.n_used):
@@ -405,7 +281,7 @@ def test_c4_prefill_chunk(blk, torch_dev, oracle, v3, zipf):
     hg, hgs = gpu_h(blk, oracle, v3, ids)
     L = oracle_layer(oracle, v3, 202, 2, ids[sub])
     # the subset's h rows, as the check's GPU taps
-    blk_sub = _Taps(hg[sub], hgs[sub])
+    blk_sub = Taps(hg[sub], hgs[sub])
     check_block(oracle, L, blk_sub, v3, x[sub], ids[sub], wts[sub], got[sub], "C4")
 
 
@@ -541,11 +417,10 @@ def test_split_compute_with_clamps(blk, oracle):
         blk.split_compute(sg.split_nodes(g, nd))
         ref = blk.forward_host(8, x, ids, wts, flags=mb.MOE_FWD_PER_SLOT)
         assert np.array_equal(out.view(np.uint32), ref.view(np.uint32))
-        # a sanity bound only: the block's own parity (with Q8_0 boundary tokens
-        # handled) is test_clamp_active's; this split equals the block bit for bit
+        # the MUL node against the oracle's at the contract's 1e-3 (the taps are
+        # the forward_host call's: the same inputs, the same h)
         L = oracle_layer(oracle, shape, 57, 8, ids, e_lo=128, e_span=3)
-        o = L.forward(x, ids, wts, per_slot=True)["per_slot"]
-        assert_rms_close(out, o, tol=2e-2, what="split with clamps vs oracle MUL node")
+        check_block(oracle, L, blk, shape, x, ids, wts, out, "split with clamps", per_slot=True)
     finally:
         blk.release_layer(8)
 
@@ -624,3 +499,55 @@ def test_budget_accounting(torch_dev):
             b.generate_layer(1, wl.C1, seed=1)
         b.release_layer(0)
         b.generate_layer(1, wl.C1, seed=1)
+
+
+# ---- live graphs keep their memory ------------------------------------------------------------
+
+def test_live_graph_pins_scratch_and_layers(torch_dev, oracle):
+    """While a captured graph is alive, the calls that would free or move the
+    memory it replays are refused on the host (MOE_ERR_INVALID_ARG, nothing
+    launched): a forward or reserve that needs a larger scratch, and the
+    release of a captured layer.  A layer the graph does not read can still
+    be released; after the graph is destroyed everything works again; a
+    graph whose context was destroyed is refused at launch."""
+    torch, dev = torch_dev
+    say("live graph guard")
+    b = mb.MoeBlock(0)
+    try:
+        b.generate_layer(0, wl.C1, seed=11)
+        b.generate_layer(1, wl.C1, seed=12)
+        b.reserve(wl.C1, 1)
+        x, lg = wl.make_inputs(wl.C1, 4, 5)
+        ids, wts = oracle.route(lg, wl.C1.n_used, wl.C1.route_mode, norm=True)
+        xd, idd, wd = (torch.from_numpy(a).to(dev) for a in (x, ids, wts))
+        out1 = torch.zeros((1, wl.C1.hidden), dtype=torch.float32, device=dev)
+        b.forward(0, xd[:1], idd[:1], wd[:1], out1)
+        torch.cuda.synchronize()
+        eager = out1.cpu().numpy().copy()
+        g = b.graph_capture([0], [xd[:1]], [idd[:1]], [wd[:1]], [out1])
+        out4 = torch.zeros((4, wl.C1.hidden), dtype=torch.float32, device=dev)
+        for what, call in [("forward T=4", lambda: b.forward(0, xd, idd, wd, out4)),
+                           ("reserve T=4", lambda: b.reserve(wl.C1, 4)),
+                           ("forward_host T=4", lambda: b.forward_host(0, x, ids, wts)),
+                           ("release captured layer", lambda: b.release_layer(0))]:
+            with pytest.raises(mb.MoeError) as ei:
+                call()
+            assert ei.value.status == mb.MOE_ERR_INVALID_ARG, what
+            say(what, "refused:", str(ei.value)[:100])
+        b.release_layer(1)  # not read by the graph
+        out1.zero_()
+        g.launch()
+        torch.cuda.synchronize()
+        np.testing.assert_array_equal(out1.cpu().numpy(), eager)
+        g.close()
+        b.forward(0, xd, idd, wd, out4)  # the scratch may grow again
+        b.release_layer(0)
+        torch.cuda.synchronize()
+        b.generate_layer(0, wl.C1, seed=11)
+        g2 = b.graph_capture([0], [xd], [idd], [wd], [out4])
+    finally:
+        b.close()
+    with pytest.raises(mb.MoeError) as ei:
+        g2.launch()
+    assert ei.value.status == mb.MOE_ERR_INVALID_ARG
+    g2.close()

@@ -5,9 +5,13 @@ bf16 and f16 routers, a selection bias on layer 1 and an MXFP4 shared
 expert the server must leave to the trunk) is written from the generator's
 blocks.  Every response is checked bit-exact against the same library
 driven directly (moe_router_logits -> moe_route_forward with
-MOE_FWD_NO_SHARED): the block's own parity with the oracle, and the ids'
-bit-exactness, are covered by test_gpu_block.py.  The router logits are
-checked against float64 numpy.  Error responses follow moe-server's checks
+MOE_FWD_NO_SHARED), and that against the CPU oracle: the oracle's routing
+of the GPU's router logits gives the same ids, and the oracle's block on
+those ids (routed experts only) matches the rows within 1e-3 of their RMS.
+The router logits are checked against float64 numpy with x rounded to the
+router's type first (ggml-cpu's mul_mat converts x to an f16 / bf16
+weight's type; the products are then exact, so only the f32 summation
+order can differ).  Error responses follow moe-server's checks
 (nano-glm/apps/moe-server/main.cpp:815-852), over handle() and over TCP.
 """
 import socket
@@ -19,6 +23,7 @@ import pytest
 import gguf_stub as gs
 import moe_block as mb
 import workloads as wl
+from parity import check_block, oracle_layer
 
 pytestmark = pytest.mark.gpu
 
@@ -63,7 +68,7 @@ def model(tmp_path_factory, oracle):
             w = w16.astype(np.float32)  # f16 -> f32 is exact
             bias = None
             tensors.append((f"blk.{il}.ffn_gate_inp.weight", [H, E], gs.GGML_F16, w16.tobytes()))
-        routers[il] = (w, bias)
+        routers[il] = (w, bias, {1: mb.GGML_F32, 2: mb.GGML_BF16, 3: mb.GGML_F16}[il])
     path = tmp_path_factory.mktemp("srv") / "glm-moe.gguf"
     path.write_bytes(gs.gguf_bytes(kvs, tensors))
     say("server model", path.stat().st_size, "bytes")
@@ -82,6 +87,7 @@ def direct(model, torch_dev):
     """The same layers in a plain MoeBlock context (ids 101-103)."""
     path, _ = model
     b = mb.MoeBlock(0)
+    b.set_taps(True)
     for il in (1, 2, 3):
         info = b.upload_layer_gguf(100 + il, path, il)
         assert info.desc.has_shared == (1 if il == 1 else 0)
@@ -110,21 +116,31 @@ def parse_response(r: bytes):
     return h, r[56:]
 
 
+def round_to(x: np.ndarray, w_type: int) -> np.ndarray:
+    """x rounded to the router's ggml type (round to nearest even), as f32."""
+    if w_type == mb.GGML_F16:
+        return x.astype(np.float16).astype(np.float32)
+    if w_type == mb.GGML_BF16:
+        return (to_bf16_bits(x).astype(np.uint32) << 16).view(np.float32)
+    return x
+
+
 def reference(direct, torch_dev, routers, layer, x):
-    """Router logits and combined routed rows through the library directly."""
+    """Router logits, ids, weights and combined routed rows through the
+    library directly."""
     torch, dev = torch_dev
-    w, bias = routers[layer]
+    w, bias, w_type = routers[layer]
     T = x.shape[0]
     xd = torch.from_numpy(x).to(dev)
     lg = torch.empty((T, E), dtype=torch.float32, device=dev)
-    direct.router_logits(torch.from_numpy(w).to(dev), xd, lg)
+    direct.router_logits(torch.from_numpy(w).to(dev), xd, lg, w_type=w_type)
     ids = torch.empty((T, K), dtype=torch.int32, device=dev)
     wts = torch.empty((T, K), dtype=torch.float32, device=dev)
     out = torch.empty((T, H), dtype=torch.float32, device=dev)
     direct.route_forward(100 + layer, xd, lg, ids, wts, out, mb.ROUTE_SIGMOID, norm=True, scale=2.5,
                          bias=None if bias is None else torch.from_numpy(bias).to(dev), flags=mb.MOE_FWD_NO_SHARED)
     torch.cuda.synchronize()
-    return lg.cpu().numpy(), out.cpu().numpy()
+    return lg.cpu().numpy(), ids.cpu().numpy(), wts.cpu().numpy(), out.cpu().numpy()
 
 
 def test_hello(server):
@@ -143,14 +159,36 @@ def test_request_matches_the_block(server, direct, model, torch_dev, layer, T):
     h, body = parse_response(server.handle(request(layer, x)))
     assert (h.status, h.n_embd, h.n_tokens, h.n_slots) == (mb.WIRE_OK, H, T, 0), body[:200]
     got = np.frombuffer(body, np.float32).reshape(T, H)
-    lg, ref = reference(direct, torch_dev, model[1], layer, x)
-    w = model[1][layer][0].astype(np.float64)
-    lg64 = x.astype(np.float64) @ w.T
+    lg, ids, wts, ref = reference(direct, torch_dev, model[1], layer, x)
+    w, bias, w_type = model[1][layer]
+    lg64 = round_to(x, w_type).astype(np.float64) @ w.astype(np.float64).T
     err = np.abs(lg - lg64).max() / np.abs(lg64).max()
-    say(f"router logits max rel err {err:.2e}; timings parse/route/compute us", h.t_parse_us, h.t_route_us,
-        h.t_compute_us)
-    assert err < 1e-5
+    say(f"router logits (type {w_type}) max rel err {err:.2e}; timings parse/route/compute us", h.t_parse_us,
+        h.t_route_us, h.t_compute_us)
+    assert err < 1e-5  # without x rounded to bf16 / f16 the difference would be ~1e-3
     assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+
+
+@pytest.mark.parametrize("layer, T", [(1, 1), (1, 6), (2, 5), (3, 3)])
+def test_response_rows_match_the_oracle(server, direct, model, torch_dev, oracle, layer, T):
+    """The server's rows against the CPU oracle: the oracle routes the GPU's
+    router logits (sigmoid, selection bias, renorm, scale 2.5) to the same
+    ids, and its block on those ids without the shared expert matches the
+    rows at 1e-3 of their RMS (parity.check_block, the direct block's h
+    taps: the rows are bit-exact with it)."""
+    x, _ = wl.make_inputs(SHAPE, T, 700 + 10 * layer + T)
+    h, body = parse_response(server.handle(request(layer, x)))
+    assert h.status == mb.WIRE_OK, body[:200]
+    got = np.frombuffer(body, np.float32).reshape(T, H)
+    lg, ids, wts, ref = reference(direct, torch_dev, model[1], layer, x)
+    assert np.array_equal(got.view(np.uint32), ref.view(np.uint32))
+    w, bias, _ = model[1][layer]
+    oi, ow = oracle.route(lg, K, mb.ROUTE_SIGMOID, norm=True, scale=2.5, bias=bias)
+    np.testing.assert_array_equal(ids, oi)
+    np.testing.assert_allclose(wts, ow, rtol=2e-6)  # the score's exp may differ by an ulp
+    say(f"server layer {layer} T={T}: ids equal the oracle's routing of the logits", oi.tolist()[:2])
+    L = oracle_layer(oracle, SHAPE, SEED, layer, oi)
+    check_block(oracle, L, direct, SHAPE, x, oi, ow, got, f"server layer {layer} T{T}")
 
 
 @pytest.mark.parametrize("case, status", [
@@ -255,7 +293,7 @@ def test_deepseek4_model(tmp_path, oracle, torch_dev):
         w = np.frombuffer(tensors[-1][3], np.float32).reshape(E, H)
         xd = torch.from_numpy(x).to(dev)
         lg = torch.empty((4, E), dtype=torch.float32, device=dev)
-        blk.router_logits(torch.from_numpy(w.copy()).to(dev), xd, lg)
+        blk.router_logits(torch.from_numpy(w.copy()).to(dev), xd, lg, w_type=mb.GGML_F32)
         ids = torch.empty((4, K), dtype=torch.int32, device=dev)
         wts = torch.empty((4, K), dtype=torch.float32, device=dev)
         out = torch.empty((4, H), dtype=torch.float32, device=dev)
