@@ -379,6 +379,23 @@ moe_status moe_forward(moe_ctx *ctx, int layer, const float *x_dev,
                        const int32_t *ids_dev, const float *wts_dev, int T,
                        float *out_dev, uint32_t flags, void *stream);
 
+/* moe_forward that allocates nothing.  No counterpart in the reference: it
+ * is for callers that cannot allocate device memory during a call (code
+ * under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  Same arguments, kernels and results as moe_forward; the
+ * per-call buffers come from one file-scope device array of
+ * MOE_NOALLOC_SCRATCH_BYTES per GPU, held from the first moe_ctx_create on
+ * that GPU until the process ends, instead of the context's scratch.  A
+ * call whose buffers do not fit (T > 213 tokens on a V3-shaped
+ * layer) returns MOE_ERR_INVALID_ARG.  Every call on one GPU shares that
+ * GPU's array, across contexts: calls that overlap in time on one GPU
+ * (other streams, other threads) race and give wrong results.  No HIP
+ * event profiling and no debug taps on this path. */
+#define MOE_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+moe_status moe_forward_noalloc(moe_ctx *ctx, int layer, const float *x_dev,
+                               const int32_t *ids_dev, const float *wts_dev, int T,
+                               float *out_dev, uint32_t flags, void *stream);
+
 /* moe_forward from host buffers, synchronous: the reference's per-call
  * boundary (stage x/ids/wts in, read the result back into the host MUL
  * node, moe_tp.h:726-777). */

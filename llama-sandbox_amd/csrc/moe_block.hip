@@ -22,6 +22,7 @@
 #include <cstdlib>
 #include <cstring>
 #include <map>
+#include <mutex>
 #include <set>
 #include <string>
 #include <vector>
@@ -106,6 +107,10 @@ struct moe_ctx {
   // weights of the layers it captured, so while one is alive the scratch is
   // never reallocated and those layers are never released.
   std::set<moe_graph *> graphs;
+  // this device's copy of the file-scope no-allocation scratch (null if its
+  // set-up failed; noalloc_err says why)
+  uint8_t *noalloc = nullptr;
+  std::string noalloc_err;
 };
 
 // HIP-event pair around one kernel launch while profiling is on (never
@@ -270,6 +275,91 @@ static moe_status scratch_reserve(moe_ctx *c, int T, int H, int F, int E, int k)
 }
 
 // ---------------------------------------------------------------------------
+// The no-allocation entry point's scratch (moe_forward_noalloc): one
+// file-scope device array, so that a call allocates nothing.  Every GPU the
+// library runs on holds its own copy (MOE_NOALLOC_SCRATCH_BYTES) until the
+// process ends.  Host code never uses the array's name as a device address:
+// hipGetSymbolAddress gives each device's address once, at the first
+// moe_ctx_create on that device, and that pointer is what the kernels get.
+// Layout for one call: [ticks: MOE_NOALLOC_TICK_BYTES][part][hq][hd][y][xq][xd]
+// [grouping workspace], each 256-byte aligned.  The ticks must be zero when a
+// gate/up launch starts; they are cleared once here, and every launch that
+// counts on a tick returns it to zero.
+
+#define MOE_NOALLOC_TICK_BYTES ((size_t)64 << 10)
+#define MOE_MAX_DEVICES 64
+
+static __device__ __align__(256) uint8_t scratch[MOE_NOALLOC_SCRATCH_BYTES];
+
+static std::mutex g_noalloc_mu;
+static uint8_t *g_noalloc_ptr[MOE_MAX_DEVICES];
+
+__global__ void k_fill_zero(uint32_t *__restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = 0u;
+}
+
+// Once per device, with that device current.
+static void noalloc_setup(moe_ctx *c) {
+  std::lock_guard<std::mutex> lk(g_noalloc_mu);
+  if (c->device >= MOE_MAX_DEVICES) {
+    c->noalloc_err = "device index beyond the no-allocation table";
+    return;
+  }
+  if (!g_noalloc_ptr[c->device]) {
+    void *p = nullptr;
+    hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      c->noalloc_err = std::string("hipGetSymbolAddress(scratch) failed: ") + hipGetErrorString(e);
+      return;
+    }
+    hipLaunchKernelGGL(k_fill_zero, dim3(64), dim3(256), 0, 0, (uint32_t *)p, MOE_NOALLOC_TICK_BYTES / 4);
+    e = hipGetLastError();
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+      c->noalloc_err = std::string("clearing the no-allocation ticks failed: ") + hipGetErrorString(e);
+      return;
+    }
+    g_noalloc_ptr[c->device] = (uint8_t *)p;
+  }
+  c->noalloc = g_noalloc_ptr[c->device];
+}
+
+// Carve one call's buffers out of the no-allocation scratch at base; returns
+// the bytes they need (buffers are set only when that fits the array).
+static size_t noalloc_layout(uint8_t *base, int T, int H, int F, int E, int k, work_bufs &s) {
+  const size_t P = (size_t)T * k, R = P + T;
+  size_t off = MOE_NOALLOC_TICK_BYTES;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off = (off + bytes + 255) & ~(size_t)255;
+    return base + at;
+  };
+  uint8_t *part = take((size_t)16 * (F / 32) * 4 * 16 * 4);
+  uint8_t *hq = take(R * (F / 32) * 64);
+  uint8_t *hd = take(R * (F / 32) * 4);
+  uint8_t *y = take(R * H * 4);
+  uint8_t *xq = take((size_t)T * (H / 32) * 64);
+  uint8_t *xd = take((size_t)T * (H / 32) * 4);
+  const size_t grp_words = group_ws_words(T, k, E);
+  uint8_t *grp = take(grp_words * 4);
+  const bool ticks_fit = (size_t)16 * (F / 32) * 4 <= MOE_NOALLOC_TICK_BYTES;
+  if (off > MOE_NOALLOC_SCRATCH_BYTES || !ticks_fit) return ticks_fit ? off : SIZE_MAX;
+  s = work_bufs();
+  s.T = T; s.H = H; s.F = F; s.E = E; s.k = k;
+  s.tick = reinterpret_cast<int *>(base);
+  s.part = reinterpret_cast<float *>(part);
+  s.hq = reinterpret_cast<uint32_t *>(hq);
+  s.hd = reinterpret_cast<float *>(hd);
+  s.y = reinterpret_cast<float *>(y);
+  s.xq = reinterpret_cast<uint32_t *>(xq);
+  s.xd = reinterpret_cast<float *>(xd);
+  s.grp = reinterpret_cast<int32_t *>(grp);
+  s.grp_words = grp_words;
+  s.timed = false;  // the profiler's events would be created on demand: not here
+  return off;
+}
+
+// ---------------------------------------------------------------------------
 // context
 
 extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx **out) {
@@ -294,6 +384,7 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
 
   c->budget = (inject & 2) ? 0 : budget_bytes;
   c->inject = inject;
+  noalloc_setup(c);
   *out = c;
   return MOE_OK;
 }
@@ -812,6 +903,30 @@ extern "C" moe_status moe_forward(moe_ctx *c, int layer, const float *x, const i
   if (st != MOE_OK) return st;
   if (T == 1) return forward_decode(c, L, c->sc, x, ids, wts, out, flags, (hipStream_t)stream);
   return forward_grouped(c, L, c->sc, x, ids, wts, T, out, flags, (hipStream_t)stream);
+}
+
+extern "C" moe_status moe_forward_noalloc(moe_ctx *c, int layer, const float *x, const int32_t *ids,
+                                          const float *wts, int T, float *out, uint32_t flags, void *stream) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  if (c->inject & 1) return fail(c, MOE_ERR_INJECTED, "forward failure injected by MOE_BLOCK_INJECT");
+  if (!x || !ids || !wts || !out || T <= 0) return fail(c, MOE_ERR_INVALID_ARG, "moe_forward_noalloc: bad arguments");
+  auto it = c->layers.find(layer);
+  if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident; CPU fallback", layer);
+  if (!c->noalloc) return fail(c, MOE_ERR_HIP, "moe_forward_noalloc: %s", c->noalloc_err.c_str());
+  dev_layer &L = it->second;
+  const moe_layer_desc &d = L.d;
+  if ((long)T * d.n_used > MOE_GROUP_MAX_PAIRS)
+    return fail(c, MOE_ERR_INVALID_ARG, "moe_forward_noalloc: more than %d (token, slot) pairs", MOE_GROUP_MAX_PAIRS);
+  work_bufs s;
+  const size_t need = noalloc_layout(c->noalloc, T, d.hidden, d.ffn, d.n_expert, d.n_used, s);
+  if (!s.hq)
+    return fail(c, MOE_ERR_INVALID_ARG,
+                "moe_forward_noalloc: T=%d on this layer needs %zu bytes of scratch, more than the %zu the "
+                "library holds (MOE_NOALLOC_SCRATCH_BYTES); use moe_forward",
+                T, need, (size_t)MOE_NOALLOC_SCRATCH_BYTES);
+  if (!c->capturing) HIPC(c, hipSetDevice(c->device));
+  if (T == 1) return forward_decode(c, L, s, x, ids, wts, out, flags, (hipStream_t)stream);
+  return forward_grouped(c, L, s, x, ids, wts, T, out, flags, (hipStream_t)stream);
 }
 
 extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, const int32_t *ids,

@@ -37,7 +37,7 @@ T_GATE, T_UP, T_DOWN = 0, 1, 2
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_last_error", "moe_status_str", "moe_ctx_budget_left",
     "moe_ctx_reserve", "moe_layer_upload", "moe_layer_generate", "moe_layer_read_blocks",
-    "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward",
+    "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward", "moe_forward_noalloc",
     "moe_forward_host",
     "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
     "moe_prof_enable", "moe_prof_read", "moe_debug_set_taps",
@@ -173,6 +173,8 @@ def load_library(path: str | None = None):
     L.moe_group.argtypes = [_vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int, _vp, _vp, _vp, _vp, _vp]
     L.moe_forward.restype = st
     L.moe_forward.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, _vp, ctypes.c_uint32, _vp]
+    L.moe_forward_noalloc.restype = st
+    L.moe_forward_noalloc.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, _vp, ctypes.c_uint32, _vp]
     L.moe_forward_host.restype = st
     L.moe_forward_host.argtypes = [_vp, ctypes.c_int, _vp, _vp, _vp, ctypes.c_int, _vp, ctypes.c_uint32]
     L.moe_route_forward.restype = st
@@ -277,6 +279,9 @@ def _ptr(t) -> int | None:
 # below checks its tensors before the call and raises ValueError instead.
 # The order (dtype, shape, contiguity, device) lets the CPU tests reach each
 # refusal with host tensors.
+
+NOALLOC_SCRATCH_BYTES = 64 << 20  # MOE_NOALLOC_SCRATCH_BYTES
+
 
 def check_tensor(t, name: str, dtype: str, shape=None, device: bool = True):
     """t: a torch tensor of `dtype` ("float32", "int32", ...), `shape` (a
@@ -474,6 +479,13 @@ class MoeBlock:
         T = check_forward_args(self.descs.get(layer), x, ids, wts, out, flags)
         self._check(self.lib.moe_forward(self.h, layer, _ptr(x), _ptr(ids), _ptr(wts), T, _ptr(out), flags,
                                          _stream(stream)), "moe_forward")
+
+    def forward_noalloc(self, layer: int, x, ids, wts, out, flags: int = 0, stream=None):
+        """moe_forward_noalloc: the same block with the per-call buffers in the
+        library's file-scope device scratch (no allocation)."""
+        T = check_forward_args(self.descs.get(layer), x, ids, wts, out, flags)
+        self._check(self.lib.moe_forward_noalloc(self.h, layer, _ptr(x), _ptr(ids), _ptr(wts), T, _ptr(out), flags,
+                                                 _stream(stream)), "moe_forward_noalloc")
 
     def route_forward(self, layer: int, x, logits, ids, wts, out, mode: int, norm: bool = True,
                       scale: float = 1.0, bias=None, flags: int = 0, stream=None):

@@ -100,6 +100,7 @@ def test_methods_check_before_calling_the_library():
     bad_x = host((2, 1024))
     calls = [
         lambda: b.forward(0, bad_x, ids, wts, out),
+        lambda: b.forward_noalloc(0, bad_x, ids, wts, out),
         lambda: b.forward(0, x, host((2, 3), torch.int32), wts, out),
         lambda: b.route_forward(0, x, host((2, 16)), ids, wts, out, mode=0),       # logits of E=16, layer has 32
         lambda: b.graph_capture([0, 0], [x, x[:1]], [ids, ids[:1]], [wts, wts[:1]], [out, out[:1]]),
