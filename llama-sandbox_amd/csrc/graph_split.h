@@ -70,11 +70,11 @@ extern "C" moe_status moe_split_parse(const moe_node *const *nodes, int n, moe_s
     if (t->op == MOE_NODE_GLU) glu = t;
     if (t->op == MOE_NODE_MUL) mul = t;
   }
-  if (!glu || !mul) return split_why(why, why_len, "no GLU or MUL");
-  if (glu->glu_op != MOE_GLU_SWIGLU || glu->glu_swapped != 0) return split_why(why, why_len, "glu variant");
+  if (!glu || !mul) return split_why(why, why_len, "the split has no SwiGLU node or no router-weight multiply");
+  if (glu->glu_op != MOE_GLU_SWIGLU || glu->glu_swapped != 0) return split_why(why, why_len, "the activation is not an unswapped SwiGLU");
   // gate and up: a MUL_MAT_ID, each optionally behind a CLAMP
   const moe_node *gc = glu->src[0], *uc = glu->src[1];
-  if (!gc || !uc) return split_why(why, why_len, "glu sources missing");
+  if (!gc || !uc) return split_why(why, why_len, "the SwiGLU node lacks a gate or an up input");
   c->gate_min = c->up_min = -INFINITY;
   c->gate_max = c->up_max = INFINITY;
   const moe_node *gmm = gc, *umm = uc;
@@ -89,10 +89,10 @@ extern "C" moe_status moe_split_parse(const moe_node *const *nodes, int n, moe_s
     umm = uc->src[0];
   }
   if (!gmm || !umm || gmm->op != MOE_NODE_MUL_MAT_ID || umm->op != MOE_NODE_MUL_MAT_ID)
-    return split_why(why, why_len, "glu sources are not (clamped) mul_mat_id");
+    return split_why(why, why_len, "gate or up is not an expert matmul (optionally clamped)");
   const moe_node *dmm = mul->src[0];
-  if (!dmm || dmm->op != MOE_NODE_MUL_MAT_ID) return split_why(why, why_len, "mul src0 not mul_mat_id");
-  if (dmm->src[1] != glu) return split_why(why, why_len, "down input not glu");
+  if (!dmm || dmm->op != MOE_NODE_MUL_MAT_ID) return split_why(why, why_len, "the router-weight multiply does not take the down expert matmul");
+  if (dmm->src[1] != glu) return split_why(why, why_len, "the down expert matmul does not read the SwiGLU output");
   c->gate_w = gmm->src[0];
   c->up_w = umm->src[0];
   c->down_w = dmm->src[0];
@@ -101,32 +101,32 @@ extern "C" moe_status moe_split_parse(const moe_node *const *nodes, int n, moe_s
   c->wts = mul->src[1];
   c->out = mul;
   if (!c->gate_w || !c->up_w || !c->down_w || !c->x || !c->ids || !c->wts)
-    return split_why(why, why_len, "missing source");
+    return split_why(why, why_len, "an expert matmul or the multiply lacks an operand");
   if (umm->src[1] != c->x || umm->src[2] != c->ids || dmm->src[2] != c->ids)
-    return split_why(why, why_len, "shared x/ids mismatch");
-  if (!c->x->data || !c->ids->data || !c->wts->data || !c->out->data) return split_why(why, why_len, "missing host data");
+    return split_why(why, why_len, "gate, up and down do not read the same activations and expert ids");
+  if (!c->x->data || !c->ids->data || !c->wts->data || !c->out->data) return split_why(why, why_len, "an input or the output has no host memory behind it");
   if (c->x->type != MOE_GGML_F32 || c->ids->type != MOE_GGML_I32 || c->wts->type != MOE_GGML_F32 ||
       c->out->type != MOE_GGML_F32)
-    return split_why(why, why_len, "io types");
+    return split_why(why, why_len, "the activations, router weights or output are not f32, or the ids not i32");
   if (c->gate_w->type != MOE_GGML_MXFP4 || c->up_w->type != MOE_GGML_MXFP4 || c->down_w->type != MOE_GGML_MXFP4)
-    return split_why(why, why_len, "weight types");
+    return split_why(why, why_len, "an expert weight tensor is not MXFP4");
   if (!c->out->contiguous || !c->x->contiguous || !c->ids->contiguous || !c->wts->contiguous)
-    return split_why(why, why_len, "io not contiguous");
+    return split_why(why, why_len, "an input or the output is not contiguous");
   // shapes: gate/up [H, F, E], down [F, H, E], x [H, 1, T], ids [k, T], wts [1, k, T], out [H, k, T]
   const int64_t H = c->gate_w->ne[0], F = c->gate_w->ne[1], E = c->gate_w->ne[2];
   const int64_t k = c->ids->ne[0], T = c->ids->ne[1];
   if (c->up_w->ne[0] != H || c->up_w->ne[1] != F || c->up_w->ne[2] != E || c->down_w->ne[0] != F ||
       c->down_w->ne[1] != H || c->down_w->ne[2] != E)
-    return split_why(why, why_len, "weight shapes");
+    return split_why(why, why_len, "the gate, up and down weight shapes do not agree");
   if (c->x->ne[0] != H || c->x->ne[1] != 1 || c->x->ne[2] != T || c->wts->ne[0] != 1 || c->wts->ne[1] != k ||
       c->wts->ne[2] != T || c->out->ne[0] != H || c->out->ne[1] != k || c->out->ne[2] != T)
-    return split_why(why, why_len, "io shapes");
+    return split_why(why, why_len, "the activation, router-weight or output shapes do not match the weights");
   if (H <= 0 || F <= 0 || E <= 0 || k <= 0 || T <= 0 || H > INT32_MAX || F > INT32_MAX || E > INT32_MAX ||
       k > E || T > INT32_MAX)
-    return split_why(why, why_len, "sizes");
+    return split_why(why, why_len, "a dimension is empty, or the top-k exceeds the expert count");
   const char *name = c->gate_w->name;
   if (!name || strncmp(name, "blk.", 4) != 0 || name[4] < '0' || name[4] > '9')
-    return split_why(why, why_len, "weight name");
+    return split_why(why, why_len, "the gate weight name does not start with blk.<layer>.");
   c->layer = atoi(name + 4);
   c->n_slots = (int32_t)k;
   c->n_tokens = (int32_t)T;

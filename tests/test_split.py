@@ -90,42 +90,42 @@ def test_parse_refusals():
         return g, nd, sg.split_nodes(g, nd)
 
     g, nd, nodes = fresh()
-    _refuse([n for n in nodes if n.op != mb.NODE_GLU], "no GLU or MUL")
+    _refuse([n for n in nodes if n.op != mb.NODE_GLU], "no SwiGLU node")
     g, nd, nodes = fresh()
     nd["act"].glu_swapped = 1
-    _refuse(nodes, "glu variant")
+    _refuse(nodes, "not an unswapped SwiGLU")
     g, nd, nodes = fresh()
     nd["act"].glu_op = 0
-    _refuse(nodes, "glu variant")
+    _refuse(nodes, "not an unswapped SwiGLU")
     g, nd, nodes = fresh()
     other = g.node(mb.NODE_NONE, (H, K, T))
     nd["mul"].src[0] = mb.ctypes.pointer(other)
-    _refuse(nodes, "mul src0 not mul_mat_id")
+    _refuse(nodes, "does not take the down expert matmul")
     g, nd, nodes = fresh()
     nd["y"].src[1] = mb.ctypes.pointer(nd["gate"])
-    _refuse(nodes, "down input not glu")
+    _refuse(nodes, "does not read the SwiGLU output")
     g, nd, nodes = fresh()
     x2 = g.node(mb.NODE_NONE, (H, 1, T), data=np.zeros((T, H), np.float32))
     up_mm = nd["up"].src[0].contents  # the up clamp's source: the up mul_mat_id
     up_mm.src[1] = mb.ctypes.pointer(x2)
-    _refuse(nodes, "shared x/ids mismatch")
+    _refuse(nodes, "same activations and expert ids")
     g, nd, nodes = fresh(weight_type=8)
-    _refuse(nodes, "weight types")
+    _refuse(nodes, "not MXFP4")
     g, nd, nodes = fresh()
     nd["ids"].type = mb.GGML_F32
-    _refuse(nodes, "io types")
+    _refuse(nodes, "not f32, or the ids not i32")
     g, nd, nodes = fresh()
     nd["mul"].contiguous = 0
-    _refuse(nodes, "io not contiguous")
+    _refuse(nodes, "not contiguous")
     g, nd, nodes = fresh()
     nd["w_down"].ne[0] = F + 32
-    _refuse(nodes, "weight shapes")
+    _refuse(nodes, "weight shapes do not agree")
     g, nd, nodes = fresh()
     nd["mul"].ne[1] = K + 1
-    _refuse(nodes, "io shapes")
+    _refuse(nodes, "shapes do not match the weights")
     g, nd, nodes = fresh()
     nd["w_gate"].name = b"ffn_gate_exps.weight"
-    _refuse(nodes, "weight name")
+    _refuse(nodes, "does not start with blk.")
     g, nd, nodes = fresh()
     nd["mul"].data = None
-    _refuse(nodes, "missing host data")
+    _refuse(nodes, "no host memory behind it")
