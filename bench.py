@@ -608,6 +608,8 @@ def trace_gaps(path: str, n_layers: int = 40):
     with open(path, newline="") as f:
         for r in csv.DictReader(f):
             name = r["Kernel_Name"]
+            if name.startswith("void "):  # template instances
+                name = name[5:]
             if name.startswith("k_gate_up") or name.startswith("k_down"):
                 recs.append((int(r["Start_Timestamp"]), int(r["End_Timestamp"]), name))
     recs.sort()

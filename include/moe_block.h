@@ -452,6 +452,31 @@ typedef struct {
 } moe_kernel_stat;
 
 moe_status moe_prof_enable(moe_ctx *ctx, int on);
+
+/* Engagement and phase counters of the host-boundary calls (moe_forward_host
+ * and moe_split_compute): how many ran on the device, how many were refused
+ * (any error: the caller ran its CPU path), the distinct routed experts
+ * they read, and their phases -- upload (inputs to the device), compute
+ * (the block), read (rows back), from HIP events on the call's stream while
+ * moe_prof_enable is on, and total host time always.  The last device call's
+ * figures are kept separately, for a per-split phase record.  The
+ * reference keeps the same figures: "N splits on the dies, M fell back",
+ * per-call stage / submit / wait times (moe-serv/src/moe_tp.h:792-802) and
+ * the per-split phase rows of MOESERV_PROFILE (moe-serv/src/moe_prof.h:36-137). */
+typedef struct {
+  uint64_t calls;        /* computed on the device                          */
+  uint64_t refusals;     /* returned an error (the caller's CPU path ran)   */
+  uint64_t expert_loads; /* distinct routed experts, summed over the calls  */
+  uint64_t timed_calls;  /* calls whose phases were timed                   */
+  double upload_us, compute_us, read_us; /* summed over the timed calls     */
+  double total_us;       /* summed host time of the device calls            */
+  double last_upload_us, last_compute_us, last_read_us, last_total_us;
+  uint32_t last_experts, last_tokens, last_timed;
+} moe_call_stats;
+
+/* Copy the counters; reset != 0 clears the sums and counts (not the last
+ * call's figures). */
+moe_status moe_call_stats_read(moe_ctx *ctx, moe_call_stats *stats, int reset);
 /* Wait for the recorded launches, add them up, and return one entry per
  * kernel class with launches > 0 (at most cap, *n = the number of classes).
  * reset != 0 clears the totals afterwards. */

@@ -136,8 +136,19 @@ extern "C" moe_status moe_split_parse(const moe_node *const *nodes, int n, moe_s
   return MOE_OK;
 }
 
+static moe_status split_compute_impl(moe_ctx *c, const moe_node *const *nodes, int n);
+
+// A split the parse or the checks refuse counts as a refusal (the caller runs
+// it on the CPU); one computed on the device is counted by moe_forward_host.
 extern "C" moe_status moe_split_compute(moe_ctx *c, const moe_node *const *nodes, int n) {
   if (!c) return MOE_ERR_INVALID_ARG;
+  const uint64_t before = c->calls.refusals;
+  const moe_status st = split_compute_impl(c, nodes, n);
+  if (st != MOE_OK && c->calls.refusals == before) c->calls.refusals++;
+  return st;
+}
+
+static moe_status split_compute_impl(moe_ctx *c, const moe_node *const *nodes, int n) {
   moe_split sp;
   char why[128];
   const moe_status st = moe_split_parse(nodes, n, &sp, why, sizeof why);

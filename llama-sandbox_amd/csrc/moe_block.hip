@@ -17,6 +17,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <chrono>
 #include <cstdarg>
 #include <cstdio>
 #include <cstdlib>
@@ -89,6 +90,15 @@ struct prof_state {
   double total_us[K_COUNT] = {};
 };
 
+// Engagement and phase counters of the host-boundary calls (moe_forward_host,
+// moe_split_compute), read with moe_call_stats_read.
+struct call_state {
+  uint64_t calls = 0, refusals = 0, expert_loads = 0, timed = 0;
+  double upload_us = 0, compute_us = 0, read_us = 0, total_us = 0;
+  moe_call_stats last{};
+  hipEvent_t ev[4] = {};  // phase events, created at the first profiled call
+};
+
 struct moe_ctx {
   int device = 0;
   int n_cu = 256;
@@ -107,6 +117,7 @@ struct moe_ctx {
   // weights of the layers it captured, so while one is alive the scratch is
   // never reallocated and those layers are never released.
   std::set<moe_graph *> graphs;
+  call_state calls;
   // this device's copy of the file-scope no-allocation scratch (null if its
   // set-up failed; noalloc_err says why)
   uint8_t *noalloc = nullptr;
@@ -406,6 +417,8 @@ extern "C" void moe_ctx_destroy(moe_ctx *c) {
     (void)hipEventDestroy(r.b);
   }
   for (hipEvent_t e : c->prof.pool) (void)hipEventDestroy(e);
+  for (hipEvent_t e : c->calls.ev)
+    if (e) (void)hipEventDestroy(e);
   delete c;
 }
 
@@ -929,9 +942,80 @@ extern "C" moe_status moe_forward_noalloc(moe_ctx *c, int layer, const float *x,
   return forward_grouped(c, L, s, x, ids, wts, T, out, flags, (hipStream_t)stream);
 }
 
+// Device phases of one host-boundary call, from events on the null stream
+// (recorded only while moe_prof_enable is on).
+struct host_phases {
+  bool timed = false;
+  float upload_ms = 0, compute_ms = 0, read_ms = 0;
+};
+
+static moe_status forward_host_impl(moe_ctx *c, int layer, const float *x, const int32_t *ids, const float *wts,
+                                    int T, float *out, uint32_t flags, host_phases &ph);
+
 extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, const int32_t *ids,
                                        const float *wts, int T, float *out, uint32_t flags) {
   if (!c) return MOE_ERR_INVALID_ARG;
+  const auto t0 = std::chrono::steady_clock::now();
+  host_phases ph;
+  const moe_status st = forward_host_impl(c, layer, x, ids, wts, T, out, flags, ph);
+  call_state &cs = c->calls;
+  if (st != MOE_OK) {
+    cs.refusals++;
+    return st;
+  }
+  // distinct routed experts of the call: the expert matrices it read
+  const int k = c->layers[layer].d.n_used, E = c->layers[layer].d.n_expert;
+  std::vector<uint64_t> seen(((size_t)E + 63) / 64, 0);
+  uint32_t distinct = 0;
+  for (long i = 0; i < (long)T * k; i++) {
+    const int e = ids[i];
+    if (e < 0 || e >= E) continue;
+    if (!(seen[e >> 6] >> (e & 63) & 1)) {
+      seen[e >> 6] |= 1ull << (e & 63);
+      distinct++;
+    }
+  }
+  const double total = std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now() - t0).count();
+  cs.calls++;
+  cs.expert_loads += distinct;
+  cs.total_us += total;
+  cs.last.last_total_us = total;
+  cs.last.last_experts = distinct;
+  cs.last.last_tokens = (uint32_t)T;
+  cs.last.last_timed = ph.timed ? 1 : 0;
+  cs.last.last_upload_us = ph.timed ? 1e3 * ph.upload_ms : 0.0;
+  cs.last.last_compute_us = ph.timed ? 1e3 * ph.compute_ms : 0.0;
+  cs.last.last_read_us = ph.timed ? 1e3 * ph.read_ms : 0.0;
+  if (ph.timed) {
+    cs.timed++;
+    cs.upload_us += cs.last.last_upload_us;
+    cs.compute_us += cs.last.last_compute_us;
+    cs.read_us += cs.last.last_read_us;
+  }
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_call_stats_read(moe_ctx *c, moe_call_stats *out, int reset) {
+  if (!c || !out) return MOE_ERR_INVALID_ARG;
+  call_state &cs = c->calls;
+  *out = cs.last;
+  out->calls = cs.calls;
+  out->refusals = cs.refusals;
+  out->expert_loads = cs.expert_loads;
+  out->timed_calls = cs.timed;
+  out->upload_us = cs.upload_us;
+  out->compute_us = cs.compute_us;
+  out->read_us = cs.read_us;
+  out->total_us = cs.total_us;
+  if (reset) {
+    cs.calls = cs.refusals = cs.expert_loads = cs.timed = 0;
+    cs.upload_us = cs.compute_us = cs.read_us = cs.total_us = 0;
+  }
+  return MOE_OK;
+}
+
+static moe_status forward_host_impl(moe_ctx *c, int layer, const float *x, const int32_t *ids, const float *wts,
+                                    int T, float *out, uint32_t flags, host_phases &ph) {
   if (!x || !ids || !wts || !out || T <= 0) return fail(c, MOE_ERR_INVALID_ARG, "moe_forward_host: bad arguments");
   auto it = c->layers.find(layer);
   if (it == c->layers.end()) return fail(c, MOE_ERR_NOT_RESIDENT, "layer %d not resident; CPU fallback", layer);
@@ -958,15 +1042,30 @@ extern "C" moe_status moe_forward_host(moe_ctx *c, int layer, const float *x, co
   memcpy(c->pin, ids, bi);
   memcpy(c->pin + s.in_wts, wts, bi);
   memcpy(c->pin + s.in_x, x, bx);
+  hipEvent_t *ev = c->calls.ev;
+  if (c->prof.on && !ev[0]) {
+    for (int i = 0; i < 4; i++) HIPC(c, hipEventCreate(&ev[i]));
+  }
+  const bool timed = c->prof.on;
+  if (timed) HIPC(c, hipEventRecord(ev[0], nullptr));
   HIPC(c, hipMemcpyAsync(s.ids_in, c->pin, bin, hipMemcpyHostToDevice, nullptr));
+  if (timed) HIPC(c, hipEventRecord(ev[1], nullptr));
   st = moe_forward(c, layer, s.x_in, s.ids_in, s.wts_in, T, s.out_buf, flags, nullptr);
   if (st != MOE_OK) {
     (void)hipStreamSynchronize(nullptr);  // the staging copies finish before the next call reuses the buffer
     return st;
   }
+  if (timed) HIPC(c, hipEventRecord(ev[2], nullptr));
   HIPC(c, hipMemcpyAsync(pin_out, s.out_buf, bo, hipMemcpyDeviceToHost, nullptr));
+  if (timed) HIPC(c, hipEventRecord(ev[3], nullptr));
   HIPC(c, hipStreamSynchronize(nullptr));
   memcpy(out, pin_out, bo);
+  if (timed) {
+    HIPC(c, hipEventElapsedTime(&ph.upload_ms, ev[0], ev[1]));
+    HIPC(c, hipEventElapsedTime(&ph.compute_ms, ev[1], ev[2]));
+    HIPC(c, hipEventElapsedTime(&ph.read_ms, ev[2], ev[3]));
+    ph.timed = true;
+  }
   return MOE_OK;
 }
 

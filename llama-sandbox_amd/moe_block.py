@@ -40,7 +40,7 @@ EXPORTS = (
     "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward", "moe_forward_noalloc",
     "moe_forward_host",
     "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
-    "moe_prof_enable", "moe_prof_read", "moe_debug_set_taps",
+    "moe_prof_enable", "moe_prof_read", "moe_call_stats_read", "moe_debug_set_taps",
     "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
     "moe_gguf_read_layer", "moe_layer_upload_gguf",
     "moe_server_open", "moe_server_close", "moe_server_last_error", "moe_server_handle", "moe_server_listen",
@@ -129,6 +129,14 @@ class KernelStat(ctypes.Structure):
     _fields_ = [("name", ctypes.c_char_p), ("launches", ctypes.c_uint64), ("total_us", ctypes.c_double)]
 
 
+class CallStats(ctypes.Structure):
+    """moe_call_stats: engagement and phase counters of the host-boundary calls."""
+    _fields_ = [(n, ctypes.c_uint64) for n in ("calls", "refusals", "expert_loads", "timed_calls")] + \
+               [(n, ctypes.c_double) for n in ("upload_us", "compute_us", "read_us", "total_us", "last_upload_us",
+                                              "last_compute_us", "last_read_us", "last_total_us")] + \
+               [(n, ctypes.c_uint32) for n in ("last_experts", "last_tokens", "last_timed")]
+
+
 _vp = ctypes.c_void_p
 _lib = None
 
@@ -193,6 +201,8 @@ def load_library(path: str | None = None):
     L.moe_prof_read.restype = st
     L.moe_prof_read.argtypes = [_vp, ctypes.POINTER(KernelStat), ctypes.c_int, ctypes.POINTER(ctypes.c_int),
                                 ctypes.c_int]
+    L.moe_call_stats_read.restype = st
+    L.moe_call_stats_read.argtypes = [_vp, ctypes.POINTER(CallStats), ctypes.c_int]
     L.moe_debug_set_taps.restype = st
     L.moe_debug_set_taps.argtypes = [_vp, ctypes.c_int]
     L.moe_debug_quantize_q8_0.restype = st
@@ -542,6 +552,12 @@ class MoeBlock:
         n = ctypes.c_int()
         self._check(self.lib.moe_prof_read(self.h, arr, cap, ctypes.byref(n), int(reset)), "moe_prof_read")
         return {arr[i].name.decode(): (int(arr[i].launches), float(arr[i].total_us)) for i in range(min(n.value, cap))}
+
+    def call_stats(self, reset: bool = False) -> dict:
+        """Engagement and phase counters of the host-boundary calls (moe_call_stats_read)."""
+        cs = CallStats()
+        self._check(self.lib.moe_call_stats_read(self.h, ctypes.byref(cs), int(reset)), "moe_call_stats_read")
+        return {n: getattr(cs, n) for n, _ in CallStats._fields_}
 
     # -- test hooks -------------------------------------------------------------
     def set_taps(self, on: bool = True):

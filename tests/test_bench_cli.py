@@ -36,7 +36,7 @@ def test_trace_gaps_reads_a_kernel_trace(tmp_path):
     t = 5_000_000
     for _ in range(3):
         rows.append(("k_gate_up_bal2(int)", t, t + 20_000))
-        rows.append(("k_down_dec(int)", t + 21_000, t + 31_000))
+        rows.append(("void k_down_span<16>(int)", t + 21_000, t + 31_000))  # a template instance's name
         t += 32_000
     p = tmp_path / "k.csv"
     p.write_text(head + "".join(f'"KERNEL_DISPATCH","Agent 1",1,0,1,{i},1,"{n}",{i},{a},{b}\n'

@@ -338,9 +338,11 @@ def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
 
 # (H, F, E, k, T, shared, clamp, route): chosen so that each dispatch branch runs at
 # least once off the configs' shapes: decode k_gate_up<1> (narrow) / k_gate_up_bal2
-# (9-task workgroups) / k_gate_up_bal (other task counts); pairs (T <= 4); octets with
-# k_gate_up_o and with k_gate_up_o2 (P >= 2E, H = 256 * {8, 16, 28}); k_down_ol<6, 8,
-# 16, 28> and k_down_o (F / 128 without an instance); shared expert and clamp on and off.
+# (9-task workgroups) / k_gate_up_bal (other task counts); decode down on whole tiles
+# (k_down_dec) and on spans of fewer rows (k_down_span, more tiles than CUs); pairs
+# (T <= 4); octets with k_gate_up_o and with k_gate_up_o2 (P >= 2E, H = 256 * {8, 16,
+# 28}); k_down_ol<6, 8, 16, 28> and k_down_o (F / 128 without an instance); shared
+# expert and clamp on and off.
 SWEEP = [
     (3072, 768, 32, 4, 1, False, 0.0, wl.ROUTE_SOFTMAX),      # decode, narrow: k_gate_up<1>
     (2048, 2048, 64, 8, 1, True, 0.0, wl.ROUTE_SIGMOID),      # decode, 256 workgroups: bal2
@@ -351,6 +353,8 @@ SWEEP = [
     (1024, 1024, 256, 8, 7, True, 0.0, wl.ROUTE_SIGMOID),     # octets, k_gate_up_o, k_down_ol<8>
     (7168, 768, 16, 4, 9, False, 0.0, wl.ROUTE_SQRT_SOFTPLUS),  # o2<28>, 16-row items, k_down_ol<6>
     (2048, 3584, 8, 2, 33, True, 8.0, wl.ROUTE_SIGMOID),      # o2<8>, k_down_ol<28>, clamp
+    (5120, 2048, 32, 6, 1, True, 0.0, wl.ROUTE_SIGMOID),      # decode down on 10-row spans (k_down_span<16>)
+    (6144, 1024, 16, 4, 1, False, 3.0, wl.ROUTE_SOFTMAX),     # 12-row spans, k_down_span<8>, clamp
 ]
 
 
@@ -551,3 +555,30 @@ def test_live_graph_pins_scratch_and_layers(torch_dev, oracle):
         g2.launch()
     assert ei.value.status == mb.MOE_ERR_INVALID_ARG
     g2.close()
+
+
+def test_call_stats_count_calls_refusals_and_phases(torch_dev, oracle):
+    """moe_call_stats: host-boundary calls on the device, refusals (the
+    caller's CPU path), distinct experts read, and upload / compute / read
+    phases from events while profiling is on."""
+    say("call stats")
+    with mb.MoeBlock(0) as b:
+        b.generate_layer(0, wl.C1, seed=3)
+        x, lg = wl.make_inputs(wl.C1, 3, 8)
+        ids, wts = oracle.route(lg, wl.C1.n_used, wl.C1.route_mode, norm=True)
+        b.forward_host(0, x, ids, wts)
+        s = b.call_stats()
+        assert s["calls"] == 1 and s["refusals"] == 0 and s["timed_calls"] == 0
+        assert s["expert_loads"] == len(np.unique(ids)) == s["last_experts"] and s["last_tokens"] == 3
+        b.descs[9] = b.descs[0]  # a layer the library does not hold: refused, the caller runs its CPU path
+        with pytest.raises(mb.MoeError):
+            b.forward_host(9, x, ids, wts)
+        b.prof_enable(True)
+        b.forward_host(0, x[:1], ids[:1], wts[:1], flags=mb.MOE_FWD_PER_SLOT)
+        s = b.call_stats(reset=True)
+        assert s["calls"] == 2 and s["refusals"] == 1 and s["timed_calls"] == 1 and s["last_timed"] == 1
+        assert s["last_upload_us"] > 0 and s["last_compute_us"] > 0 and s["last_read_us"] > 0
+        assert s["last_total_us"] >= s["last_compute_us"]
+        say("phases us", s["last_upload_us"], s["last_compute_us"], s["last_read_us"], s["last_total_us"])
+        s = b.call_stats()
+        assert s["calls"] == 0 and s["refusals"] == 0 and s["last_experts"] == wl.C1.n_used
