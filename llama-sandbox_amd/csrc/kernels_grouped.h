@@ -1006,115 +1006,202 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
   else dn_ol_octets<NQ, 1>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);
 }
 
-// ---------------------------------------------------------------------------
-// Two octets per wave (items of up to 16 rows): the same weight quad feeds
-// the MFMAs of both octets from registers, so the vector-memory unit carries
-// each weight byte once per 16 tokens instead of once per 8.  The B ring is
-// one quad ahead (2 slots) to leave registers for the second octet.
-template <int NW, int NO, int NG>
-struct oring1 {
-  wq32<NW> w[4];
-  bq32<NO> b[2];
-  uint32_t sc[NG][NW][2];
+// ===========================================================================
+// Grouped gate/up with the item's B staged in LDS, chunk by chunk of K.
+//
+// One workgroup of 4 waves per (2 units of F, item of <= 16 rows): wave w
+// streams the gate (w < 2) or up (w >= 2) tile of unit 2*blockIdx.x + w%2
+// over all of K against the item's one or two octets.  The workgroup copies
+// B (the octets' x rows) into LDS in chunks of MOE_GCH quads, already in
+// MFMA lane order (the layout of stage_octet_lds, per chunk), double
+// buffered: the global loads of chunk c+1 are issued as chunk c starts and
+// written to the other buffer as it ends, then one barrier.  Every B byte
+// thus crosses the vector-memory unit once per workgroup, the waves read it
+// from LDS one step ahead, and the wave's registers hold one weight stream
+// (4 waves per SIMD).  After the K loop gate and up meet in LDS for clamp +
+// SwiGLU + Q8_0(h) as in k_gate_up_o.
+#define MOE_GCH 4                                  // quads per staged chunk
+#define MOE_GCH_STEPS (2 * MOE_GCH)                // MFMA steps per chunk
+#define MOE_GCH_OCT_U4 (MOE_GCH_STEPS * 64)        // 16-byte digit units per octet per chunk
+#define MOE_GCH_OCT_D (MOE_GCH_STEPS * 16)         // scales per octet per chunk
+#define MOE_GCH_BUF_DW (2 * MOE_GCH_OCT_U4 * 4 + 2 * MOE_GCH_OCT_D)  // dwords per chunk buffer (two octets)
+
+// This thread's part of the staging: 16-byte digit pieces of tokens
+// t = tid/64 + 4m (m < 2*NO) at block b = (tid%64)/4, piece sub = tid%4 of
+// each chunk, and the scale of token tid/16, block tid%16.
+template <int NO>
+struct gstage {
+  uint32_t xo[2 * NO];  // byte offset in the digit rows at chunk 0 (MOE_OOB: absent token)
+  int lu4[2 * NO];      // 16-byte unit in the chunk buffer
+  uint32_t dof;         // byte offset in the scale rows at chunk 0
+  int ld;               // float index in the chunk buffer
 };
 
-template <int QL, int NQW, int NW, int NO, int NG, int CPOL>
-__device__ __forceinline__ void o1fixed_from(oring1<NW, NO, NG> &r, const wstream (&ws)[NW], const aoff32 &ao,
-                                             int q0, const gsrc &src, const gsel (&gs)[NO], bool upper, int sb,
-                                             f32x16_t (&acc)[NO][NW]) {
-  if constexpr (QL < NQW) {
-    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG)
-      load_sc32<NW>(r.sc[(QL >> 2) + 1], ws, ao, (q0 >> 2) + (QL >> 2) + 1);
-    if constexpr (QL + 1 < NQW) load_bq32<NO>(r.b[(QL + 1) & 1], src, gs, q0 + QL + 1);
-    if constexpr (QL + 3 < NQW) load_wq32<NW, CPOL>(r.w[(QL + 3) & 3], ws, ao, q0 + QL + 3);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    quad_mma32<QL & 3, NW, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[QL & 1], upper, sb, acc);
-    o1fixed_from<QL + 1, NQW, NW, NO, NG, CPOL>(r, ws, ao, q0, src, gs, upper, sb, acc);
+template <int NO>
+struct gstage_regs {
+  u32x4_t v[2 * NO];
+  float d;
+};
+
+template <int NO>
+__device__ __forceinline__ gstage<NO> make_gstage(int tid, const int (&xr)[2 * NO], int xr_d, int KB) {
+  gstage<NO> g;
+  const int w = tid & 63, b = w >> 2, sub = w & 3;
+#pragma unroll
+  for (int m = 0; m < 2 * NO; m++) {
+    const int t = (tid >> 6) + 4 * m, o = t >> 3, tt = t & 7;
+    g.xo[m] = xr[m] >= 0 ? (uint32_t)((xr[m] * KB + b) * (MOE_XSW * 4) + sub * 16) : MOE_OOB;
+    g.lu4[m] = o * MOE_GCH_OCT_U4 + (b >> 1) * 64 + 32 * (sub & 1) + 4 * tt + 2 * (sub >> 1) + (b & 1);
+  }
+  const int td = tid >> 4, bd = tid & 15;
+  g.dof = xr_d >= 0 ? (uint32_t)((xr_d * KB + bd) * 4) : MOE_OOB;
+  g.ld = 2 * MOE_GCH_OCT_U4 * 4 + (td >> 3) * MOE_GCH_OCT_D + (bd >> 1) * 16 + (td & 7) * 2 + (bd & 1);
+  return g;
+}
+
+// Global loads of chunk C (blocks 16*C .. 16*C + 15 of every row).
+template <int NO, int C>
+__device__ __forceinline__ void gstage_load(gstage_regs<NO> &s, const gsrc &src, const gstage<NO> &g) {
+#pragma unroll
+  for (int m = 0; m < 2 * NO; m++)
+    s.v[m] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[m], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
+  s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
+}
+
+template <int NO>
+__device__ __forceinline__ void gstage_store(const gstage_regs<NO> &s, uint32_t *buf, const gstage<NO> &g,
+                                             int tid) {
+  u32x4_t *bu = reinterpret_cast<u32x4_t *>(buf);
+#pragma unroll
+  for (int m = 0; m < 2 * NO; m++) bu[g.lu4[m]] = s.v[m];
+  if (NO == 2 || tid < 128) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // NO == 1: tokens < 8 only
+}
+
+// LDS writes of this wave done, then the workgroup barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+template <int NO>
+__device__ __forceinline__ void load_bs32_chunk(bs32<NO> &b, const uint32_t *buf, int lane, int dlo, int ls) {
+  const u32x4_t *bl = reinterpret_cast<const u32x4_t *>(buf);
+  const float *dl = reinterpret_cast<const float *>(buf) + 2 * MOE_GCH_OCT_U4 * 4;
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    b.v[o] = bl[o * MOE_GCH_OCT_U4 + ls * 64 + lane];
+    b.d[o] = dl[o * MOE_GCH_OCT_D + ls * 16 + dlo];
   }
 }
 
-// K loop over NQW quads from q0 (q0 % 4 == 0) for NO octets, fully unrolled.
-template <int NW, int NO, int CPOL, int NQW>
-__device__ __forceinline__ void o1loop_fixed(const wstream (&ws)[NW], const aoff32 &ao, int q0, const gsrc &src,
-                                             const gsel (&gs)[NO], int lane, f32x16_t (&acc)[NO][NW]) {
+template <int NO, int NG>
+struct gring {
+  wq32<1> w[4];
+  uint32_t sc[NG][1][2];
+  bs32<NO> b[2];
+  gstage_regs<NO> stg;
+};
+
+// Quads QL .. NQ-1 of the chunked K loop.
+template <int QL, int NQ, int NO, int NG>
+__device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
+                                        const gstage<NO> &g, uint32_t *lds, int tid, int lane, int dlo, bool upper,
+                                        int sb, f32x16_t (&acc)[NO][1]) {
+  if constexpr (QL < NQ) {
+    constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH;
+    const uint32_t *buf = lds + (C & 1) * MOE_GCH_BUF_DW;
+    if constexpr (QC == 0 && C + 1 < NC) gstage_load<NO, C + 1>(r.stg, src, g);
+    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
+    if constexpr (QL + 3 < NQ) load_wq32<1, 0>(r.w[(QL + 3) & 3], ws, ao, QL + 3);
+    load_bs32_chunk<NO>(r.b[1], buf, lane, dlo, 2 * QC + 1);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step_mma32<QL & 3, 0, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[0], upper, sb, acc);
+    if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk<NO>(r.b[0], buf, lane, dlo, 2 * QC + 2);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step_mma32<QL & 3, 1, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[1], upper, sb, acc);
+    if constexpr (QC + 1 == MOE_GCH && C + 1 < NC) {
+      uint32_t *nb = lds + ((C + 1) & 1) * MOE_GCH_BUF_DW;
+      gstage_store<NO>(r.stg, nb, g, tid);
+      lds_barrier();
+      load_bs32_chunk<NO>(r.b[0], nb, lane, dlo, 0);
+    }
+    gl_from<QL + 1, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, lane, dlo, upper, sb, acc);
+  }
+}
+
+// The K loop of one wave against NO octets; leaves this wave's sums (the
+// 4 columns of a token added) in red[w%2][w/2][token][row].
+template <int NQ, int NO>
+__device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
+                                             const int (&xr)[4], int xr_d, int KB, uint32_t *lds, int tid,
+                                             int wave, int lane) {
+  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4;
+  int xrm[2 * NO];
+#pragma unroll
+  for (int m = 0; m < 2 * NO; m++) xrm[m] = xr[m];
+  const gstage<NO> g = make_gstage<NO>(tid, xrm, xr_d, KB);
+  gring<NO, NG> r;
+  // first weights in flight during the first staging
+  load_sc32<1>(r.sc[0], ws, ao, 0);
+  load_wq32<1, 0>(r.w[0], ws, ao, 0);
+  load_wq32<1, 0>(r.w[1], ws, ao, 1);
+  load_wq32<1, 0>(r.w[2], ws, ao, 2);
+  gstage_load<NO, 0>(r.stg, src, g);
+  gstage_store<NO>(r.stg, lds, g, tid);
+  lds_barrier();
+  const int n = lane & 31, gb = lane >> 5, t = n >> 2;
+  const int dlo = t * 2 + (n & 1);
+  f32x16_t acc[NO][1];
 #pragma unroll
   for (int o = 0; o < NO; o++)
 #pragma unroll
-    for (int i = 0; i < NW; i++)
+    for (int e = 0; e < 16; e++) acc[o][0][e] = 0.0f;
+  load_bs32_chunk<NO>(r.b[0], lds, lane, dlo, 0);
+  gl_from<0, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, lane, dlo, lane_upper32(lane), lane_bscale32(lane), acc);
+  lds_barrier();  // every wave is done with the chunk buffers, which now hold the sums
+  float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[o][i][e] = 0.0f;
-  constexpr int NG = (NQW + 3) / 4;
-  oring1<NW, NO, NG> r;
-  load_sc32<NW>(r.sc[0], ws, ao, q0 >> 2);
-  load_bq32<NO>(r.b[0], src, gs, q0);
-  load_wq32<NW, CPOL>(r.w[0], ws, ao, q0);
-  if constexpr (NQW > 1) load_wq32<NW, CPOL>(r.w[1], ws, ao, q0 + 1);
-  if constexpr (NQW > 2) load_wq32<NW, CPOL>(r.w[2], ws, ao, q0 + 2);
-  o1fixed_from<0, NQW, NW, NO, NG, CPOL>(r, ws, ao, q0, src, gs, lane_upper32(lane), lane_bscale32(lane), acc);
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      const float v = col4_sum(acc[o][0][e]);
+      if ((n & 3) == 0)
+        red[(((wave & 1) * 2 + (wave >> 1)) * 16 + 8 * o + (n >> 2)) * MOE_UNIT + 8 * (e >> 2) + 4 * gb + (e & 3)] = v;
+    }
 }
 
-// k_gate_up_o on items of up to 16 rows: wave w streams unit
-// 2*blockIdx.x + w%2 (gate and up) over K-half w/2 (NQH quads) against one
-// octet (items of <= 8 rows) or two (the same weight registers serve both);
-// the K-halves meet in LDS and each 32-lane half of a wave takes one (unit,
-// token) for clamp + SwiGLU + Q8_0(h), as in k_gate_up_o (same per-octet
-// sums, same bits).  grid (F/64, item capacity), 256 threads.  Requires
-// H == 256*NQH, NQH % 4 == 0.
-template <int NQH>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2)))
-void k_gate_up_o2(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
+// grid (F/64, item capacity), 256 threads, LDS 2 * MOE_GCH_BUF_DW dwords.
+// Requires H == 128 * NQ, NQ % MOE_GCH == 0.
+template <int NQ>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+void k_gate_up_ol(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
                   const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                   int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
                   float *__restrict__ htap) {
-  __shared__ __align__(16) float red[4][2][16][MOE_UNIT];  // [wave][gate/up][token][row]
+  __shared__ __align__(16) uint32_t lds[2 * MOE_GCH_BUF_DW];
   if ((int)blockIdx.y >= items[0]) return;
   const int4 it = item_of(items, blockIdx.y);
-  const int NQ4 = moe_nq4(2 * NQH), U = F / MOE_UNIT, tiles = F / MOE_TILE, KB = H / MOE_QK;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int ul = wave & 1, kp = wave >> 1, P = T * k;
-  const int u = 2 * blockIdx.x + ul;
-  const int row0 = it.y, nt = it.z;
+  constexpr int NQ4 = (NQ + 3) / 4, KB = NQ * 4;
+  const int U = F / MOE_UNIT, tiles = F / MOE_TILE;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int P = T * k, row0 = it.y, nt = it.z;
   const bool shared = it.w != 0;
-  const int q0 = kp * NQH;
-  const size_t t0 = (size_t)it.x * tiles + 2 * u;
-  const wstream ws[2] = {make_wstream32(w_g, t0, NQ4), make_wstream32(w_u, t0, NQ4)};
+  const int u = 2 * blockIdx.x + (wave & 1);
+  const wstream ws[1] = {make_wstream32((wave >> 1) ? w_u : w_g, (size_t)it.x * tiles + 2 * u, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
   const gsrc src = make_gsrc(xq, xd, T, KB);
-  gsel gs[2];
+  auto xrow = [&](int i) { return i < nt ? (shared ? row0 + i - P : perm[row0 + i] / k) : -1; };
+  int xr[4];
 #pragma unroll
-  for (int o = 0; o < 2; o++) {
-    const int i = 8 * o + ((lane & 31) >> 2);
-    int xr = -1;
-    if (i < nt) xr = shared ? row0 + i - P : perm[row0 + i] / k;
-    gs[o] = make_gsel32(lane, xr, KB);
-  }
-  const int n = lane & 31, gb = lane >> 5;
-  if (nt > 8) {
-    f32x16_t acc[2][2];
-    o1loop_fixed<2, 2, 0, NQH>(ws, ao, q0, src, gs, lane, acc);
-#pragma unroll
-    for (int o = 0; o < 2; o++)
-#pragma unroll
-      for (int i = 0; i < 2; i++)
-#pragma unroll
-        for (int e = 0; e < 16; e++) {
-          const float v = col4_sum(acc[o][i][e]);
-          if ((n & 3) == 0) red[wave][i][8 * o + (n >> 2)][8 * (e >> 2) + 4 * gb + (e & 3)] = v;
-        }
-  } else {
-    const gsel gs1[1] = {gs[0]};
-    f32x16_t acc[1][2];
-    o1loop_fixed<2, 1, 0, NQH>(ws, ao, q0, src, gs1, lane, acc);
-#pragma unroll
-    for (int i = 0; i < 2; i++)
-#pragma unroll
-      for (int e = 0; e < 16; e++) {
-        const float v = col4_sum(acc[0][i][e]);
-        if ((n & 3) == 0) red[wave][i][n >> 2][8 * (e >> 2) + 4 * gb + (e & 3)] = v;
-      }
-  }
+  for (int m = 0; m < 4; m++) xr[m] = xrow((tid >> 6) + 4 * m);
+  const int xr_d = xrow(tid >> 4);
+  if (nt > 8) gu_ol_octets<NQ, 2>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);  // uniform branch
+  else gu_ol_octets<NQ, 1>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);
   __syncthreads();
+  const float *red = reinterpret_cast<const float *>(lds);
   // (unit, token) c = 8*round + 2*wave + half-wave: unit c / 16, token c % 16
 #pragma unroll
   for (int round = 0; round < 4; round++) {
@@ -1122,9 +1209,8 @@ void k_gate_up_o2(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
     const int c = 8 * round + 2 * wave + (lane >> 5);
     const int ul2 = c >> 4, t = c & 15, j = lane & 31;
     const bool live = t < nt;
-    // waves ul2 (K-half 0) and ul2 + 2 (K-half 1) hold this unit
-    const float gsum = red[ul2][0][t][j] + red[ul2 + 2][0][t][j];
-    const float usum = red[ul2][1][t][j] + red[ul2 + 2][1][t][j];
+    const float gsum = red[((ul2 * 2 + 0) * 16 + t) * MOE_UNIT + j];
+    const float usum = red[((ul2 * 2 + 1) * 16 + t) * MOE_UNIT + j];
     const float h = live ? swiglu(gsum, usum, clamp) : 0.0f;
     const int hrow = row0 + (live ? t : 0), uu = 2 * blockIdx.x + ul2;
     h_unit_store(h, live, hs + ((size_t)hrow * U + uu) * MOE_XSW, hd + (size_t)hrow * U + uu, lane);

@@ -855,13 +855,13 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
   const bool oct = use_octets(T);
   const int BT = oct ? 8 : 4;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
-  // octets: gate/up on items of up to 16 rows (two octets per wave) where the
-  // shape has an instance and the batch averages 2 pairs per expert or more
-  // (below that most items hold one octet, and k_gate_up_o's deeper B ring
-  // is faster); down keeps items of 8 (a second item list)
+  // octets: where the shape has an instance and the batch averages 2 pairs
+  // per expert or more, gate/up (k_gate_up_ol) and down (k_down_ol2) run on
+  // a second list of items of up to 16 rows, B staged in LDS; below that most
+  // items hold one octet and the 8-row list with B from global memory is used
   int32_t *items16 = items + group_list_words(T, k, E);
   const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 2 == 0 &&
-                  (H == 256 * 28 || H == 256 * 16 || H == 256 * 8);
+                  (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
   {
@@ -876,9 +876,9 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
 #define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
 #define MOE_GU_ARGS16 L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items16, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
     const dim3 g16(F / (2 * MOE_UNIT), group_item_cap(T, k, E, 16));
-    if (o2 && H == 256 * 28) hipLaunchKernelGGL(k_gate_up_o2<28>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
-    else if (o2 && H == 256 * 16) hipLaunchKernelGGL(k_gate_up_o2<16>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
-    else if (o2 && H == 256 * 8) hipLaunchKernelGGL(k_gate_up_o2<8>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    if (o2 && H == 128 * 56) hipLaunchKernelGGL(k_gate_up_ol<56>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    else if (o2 && H == 128 * 32) hipLaunchKernelGGL(k_gate_up_ol<32>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    else if (o2 && H == 128 * 16) hipLaunchKernelGGL(k_gate_up_ol<16>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
     else if (oct) hipLaunchKernelGGL(k_gate_up_o, dim3(F / (2 * MOE_UNIT), cap), dim3(256), 0, st, MOE_GU_ARGS);
     else hipLaunchKernelGGL(k_gate_up_g<2>, dim3(F / MOE_UNIT, cap), dim3(256), 0, st, MOE_GU_ARGS);
 #undef MOE_GU_ARGS

@@ -114,8 +114,8 @@ def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
 
 def test_c1_grouped_two_octets_per_wave(blk, torch_dev, oracle, c1):
     """T = 40 on C1 (160 pairs over 32 experts, >= 2 per expert on average):
-    gate/up runs on items of up to 16 rows with two octets per wave
-    (k_gate_up_o2), down on items of up to 8; items of both sizes occur."""
+    gate/up and down run on items of up to 16 rows with one or two octets per
+    wave (k_gate_up_ol, k_down_ol2); items of both sizes occur."""
     x, lg = wl.make_inputs(c1, 40, 23, zipf=True)
     ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
     counts = np.bincount(ids.ravel(), minlength=c1.n_expert)
@@ -288,7 +288,7 @@ def test_c4_prefill_chunk(blk, torch_dev, oracle, v3, zipf):
 @pytest.mark.parametrize("T", [16, 64])
 def test_graph_replay_grouped(blk, torch_dev, oracle, v3, T):
     """A grouped call captured in a graph (T=16: k_gate_up_o on the 8-row items;
-    T=64: k_gate_up_o2 on the second, 16-row item list): every replay equals
+    T=64: k_gate_up_ol and k_down_ol2 on the 16-row item list): every replay equals
     the eager call."""
     torch, dev = torch_dev
     say("graph capture grouped T", T)
@@ -339,20 +339,20 @@ def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
 # (H, F, E, k, T, shared, clamp, route): chosen so that each dispatch branch runs at
 # least once off the configs' shapes: decode k_gate_up<1> (narrow) / k_gate_up_bal2
 # (9-task workgroups) / k_gate_up_bal (other task counts); decode down (k_down_dec) at
-# several H / F; pairs (T <= 4); octets with k_gate_up_o and with k_gate_up_o2 (P >= 2E,
-# H = 256 * {8, 16, 28}); down on 16-row items with one and two octets (k_down_ol2<6, 8,
-# 16>, with k_gate_up_o2), k_down_ol<8, 28> and k_down_o (F / 128 without an instance);
+# several H / F; pairs (T <= 4); octets with k_gate_up_o and with k_gate_up_ol (P >= 2E,
+# H = 128 * {16, 32, 56}); down on 16-row items with one and two octets (k_down_ol2<6, 8,
+# 16>, with k_gate_up_ol), k_down_ol<8, 28> and k_down_o (F / 128 without an instance);
 # shared expert and clamp on and off.
 SWEEP = [
     (3072, 768, 32, 4, 1, False, 0.0, wl.ROUTE_SOFTMAX),      # decode, narrow: k_gate_up<1>
     (2048, 2048, 64, 8, 1, True, 0.0, wl.ROUTE_SIGMOID),      # decode, 256 workgroups: bal2
     (1024, 2048, 16, 5, 1, False, 4.0, wl.ROUTE_SIGMOID),     # decode, 1280 tasks: k_gate_up_bal
     (1024, 3584, 8, 2, 3, False, 0.0, wl.ROUTE_SOFTMAX),      # pairs, F = 3584
-    (4096, 1024, 64, 6, 32, True, 0.0, wl.ROUTE_SIGMOID),     # octets, o2<16>, k_down_ol2<8> (one octet)
-    (2048, 1536, 16, 2, 20, False, 6.0, wl.ROUTE_SOFTMAX),    # octets, o2<8>, k_down_o
+    (4096, 1024, 64, 6, 32, True, 0.0, wl.ROUTE_SIGMOID),     # octets, ol<32>, k_down_ol2<8> (one octet)
+    (2048, 1536, 16, 2, 20, False, 6.0, wl.ROUTE_SOFTMAX),    # octets, ol<16>, k_down_o
     (1024, 1024, 256, 8, 7, True, 0.0, wl.ROUTE_SIGMOID),     # octets, k_gate_up_o, k_down_ol<8>
-    (7168, 768, 16, 4, 9, False, 0.0, wl.ROUTE_SQRT_SOFTPLUS),  # o2<28>, 16-row items, k_down_ol2<6>
-    (2048, 3584, 8, 2, 33, True, 8.0, wl.ROUTE_SIGMOID),      # o2<8>, k_down_ol<28>, clamp
+    (7168, 768, 16, 4, 9, False, 0.0, wl.ROUTE_SQRT_SOFTPLUS),  # ol<56>, 16-row items, k_down_ol2<6>
+    (2048, 3584, 8, 2, 33, True, 8.0, wl.ROUTE_SIGMOID),      # ol<16>, k_down_ol<28>, clamp
     (5120, 2048, 32, 6, 1, True, 0.0, wl.ROUTE_SIGMOID),      # decode, H = 5120
     (6144, 1024, 16, 4, 1, False, 3.0, wl.ROUTE_SOFTMAX),     # decode, H = 6144, clamp
     (4096, 1024, 16, 4, 64, True, 0.0, wl.ROUTE_SIGMOID),     # k_down_ol2<8>, two octets, shared rows
