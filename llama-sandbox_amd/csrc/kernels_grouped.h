@@ -1006,6 +1006,58 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
   else dn_ol_octets<NQ, 1>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);
 }
 
+// B of one step as both 16-byte halves of each octet's MFMA operand, read
+// from LDS where each step's 64 lanes are followed by a 16-byte zero slot
+// (stride 65): the half that carries no data reads the zero slot, so the
+// block-diagonal operand needs no selects.
+template <int NO>
+struct bs32z {
+  u32x4_t lo[NO], hi[NO];
+  float d[NO];
+};
+
+// Per-lane offsets (16-byte units within a step) of the two operand halves:
+// a lane of an odd column (block 2s+1) carries its data in the upper half.
+struct zoff {
+  int lo, hi;
+};
+
+__device__ __forceinline__ zoff make_zoff(int lane) {
+  const bool upper = lane_upper32(lane);
+  return zoff{upper ? 64 : lane, upper ? lane : 64};
+}
+
+template <int NO, int OB, int OD>
+__device__ __forceinline__ void load_bs32z_lds(bs32z<NO> &b, const u32x4_t *bl, const float *dl, const zoff &z,
+                                               int dlo, int step) {
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    b.lo[o] = bl[o * OB + step * 65 + z.lo];
+    b.hi[o] = bl[o * OB + step * 65 + z.hi];
+    b.d[o] = dl[o * OD + step * 16 + dlo];
+  }
+}
+
+// step_mma32 on a bs32z operand (same sequence, same bits).
+template <int SEL, int J, int NO>
+__device__ __forceinline__ void step_mma32z(const wq32<1> &w, const uint32_t (&sc)[1][2], const bs32z<NO> &b, int sb,
+                                            f32x16_t (&acc)[NO][1]) {
+  const u32x4_t a4 = w.w[0][J];
+  const i32x8_t a = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    const u32x4_t l = b.lo[o], h = b.hi[o];
+    const i32x8_t bv = {(int)l.x, (int)l.y, (int)l.z, (int)l.w, (int)h.x, (int)h.y, (int)h.z, (int)h.w};
+    f32x16_t z;
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
+    const f32x16_t r = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bv, z, 4, 0, SEL, (int)sc[0][J], 0, sb);
+    acc[o][0] = acc[o][0] + b.d[o] * r;
+  }
+#pragma unroll
+  for (int o = 0; o < NO; o++) asm volatile("" : "+v"(acc[o][0]));
+}
+
 // ===========================================================================
 // Grouped gate/up with the item's B staged in LDS, chunk by chunk of K.
 //
@@ -1013,16 +1065,18 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 // streams the gate (w < 2) or up (w >= 2) tile of unit 2*blockIdx.x + w%2
 // over all of K against the item's one or two octets.  The workgroup copies
 // B (the octets' x rows) into LDS in chunks of MOE_GCH quads, already in
-// MFMA lane order (the layout of stage_octet_lds, per chunk), double
-// buffered: the global loads of chunk c+1 are issued as chunk c starts and
-// written to the other buffer as it ends, then one barrier.  Every B byte
-// thus crosses the vector-memory unit once per workgroup, the waves read it
-// from LDS one step ahead, and the wave's registers hold one weight stream
-// (4 waves per SIMD).  After the K loop gate and up meet in LDS for clamp +
-// SwiGLU + Q8_0(h) as in k_gate_up_o.
+// MFMA lane order (the layout of stage_octet_lds, per chunk, each step's 64
+// lanes followed by a 16-byte zero slot), double buffered: the global loads
+// of chunk c+1 are issued as chunk c starts and written to the other buffer
+// as it ends, then one barrier.  Every B byte thus crosses the vector-memory
+// unit once per workgroup; the waves read both halves of each MFMA operand
+// from LDS one step ahead (the half without data from the zero slot, so no
+// selects), and a wave's registers hold one weight stream (3 waves per
+// SIMD).  After the K loop gate and up meet in LDS for clamp + SwiGLU +
+// Q8_0(h) as in k_gate_up_o.
 #define MOE_GCH 4                                  // quads per staged chunk
 #define MOE_GCH_STEPS (2 * MOE_GCH)                // MFMA steps per chunk
-#define MOE_GCH_OCT_U4 (MOE_GCH_STEPS * 64)        // 16-byte digit units per octet per chunk
+#define MOE_GCH_OCT_U4 (MOE_GCH_STEPS * 65)        // 16-byte units per octet per chunk (digits, zero slots)
 #define MOE_GCH_OCT_D (MOE_GCH_STEPS * 16)         // scales per octet per chunk
 #define MOE_GCH_BUF_DW (2 * MOE_GCH_OCT_U4 * 4 + 2 * MOE_GCH_OCT_D)  // dwords per chunk buffer (two octets)
 
@@ -1051,7 +1105,7 @@ __device__ __forceinline__ gstage<NO> make_gstage(int tid, const int (&xr)[2 * N
   for (int m = 0; m < 2 * NO; m++) {
     const int t = (tid >> 6) + 4 * m, o = t >> 3, tt = t & 7;
     g.xo[m] = xr[m] >= 0 ? (uint32_t)((xr[m] * KB + b) * (MOE_XSW * 4) + sub * 16) : MOE_OOB;
-    g.lu4[m] = o * MOE_GCH_OCT_U4 + (b >> 1) * 64 + 32 * (sub & 1) + 4 * tt + 2 * (sub >> 1) + (b & 1);
+    g.lu4[m] = o * MOE_GCH_OCT_U4 + (b >> 1) * 65 + 32 * (sub & 1) + 4 * tt + 2 * (sub >> 1) + (b & 1);
   }
   const int td = tid >> 4, bd = tid & 15;
   g.dof = xr_d >= 0 ? (uint32_t)((xr_d * KB + bd) * 4) : MOE_OOB;
@@ -1085,50 +1139,46 @@ __device__ __forceinline__ void lds_barrier() {
 }
 
 template <int NO>
-__device__ __forceinline__ void load_bs32_chunk(bs32<NO> &b, const uint32_t *buf, int lane, int dlo, int ls) {
-  const u32x4_t *bl = reinterpret_cast<const u32x4_t *>(buf);
-  const float *dl = reinterpret_cast<const float *>(buf) + 2 * MOE_GCH_OCT_U4 * 4;
-#pragma unroll
-  for (int o = 0; o < NO; o++) {
-    b.v[o] = bl[o * MOE_GCH_OCT_U4 + ls * 64 + lane];
-    b.d[o] = dl[o * MOE_GCH_OCT_D + ls * 16 + dlo];
-  }
+__device__ __forceinline__ void load_bs32_chunk(bs32z<NO> &b, const uint32_t *buf, const zoff &z, int dlo, int ls) {
+  load_bs32z_lds<NO, MOE_GCH_OCT_U4, MOE_GCH_OCT_D>(b, reinterpret_cast<const u32x4_t *>(buf),
+                                                    reinterpret_cast<const float *>(buf) + 2 * MOE_GCH_OCT_U4 * 4, z,
+                                                    dlo, ls);
 }
 
 template <int NO, int NG>
 struct gring {
   wq32<1> w[4];
   uint32_t sc[NG][1][2];
-  bs32<NO> b[2];
+  bs32z<NO> b[2];
   gstage_regs<NO> stg;
 };
 
 // Quads QL .. NQ-1 of the chunked K loop.
 template <int QL, int NQ, int NO, int NG>
 __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
-                                        const gstage<NO> &g, uint32_t *lds, int tid, int lane, int dlo, bool upper,
-                                        int sb, f32x16_t (&acc)[NO][1]) {
+                                        const gstage<NO> &g, uint32_t *lds, int tid, const zoff &z, int dlo, int sb,
+                                        f32x16_t (&acc)[NO][1]) {
   if constexpr (QL < NQ) {
     constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH;
     const uint32_t *buf = lds + (C & 1) * MOE_GCH_BUF_DW;
     if constexpr (QC == 0 && C + 1 < NC) gstage_load<NO, C + 1>(r.stg, src, g);
     if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
     if constexpr (QL + 3 < NQ) load_wq32<1, 0>(r.w[(QL + 3) & 3], ws, ao, QL + 3);
-    load_bs32_chunk<NO>(r.b[1], buf, lane, dlo, 2 * QC + 1);
+    load_bs32_chunk<NO>(r.b[1], buf, z, dlo, 2 * QC + 1);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32<QL & 3, 0, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[0], upper, sb, acc);
-    if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk<NO>(r.b[0], buf, lane, dlo, 2 * QC + 2);
+    step_mma32z<QL & 3, 0, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[0], sb, acc);
+    if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk<NO>(r.b[0], buf, z, dlo, 2 * QC + 2);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32<QL & 3, 1, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[1], upper, sb, acc);
+    step_mma32z<QL & 3, 1, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[1], sb, acc);
     if constexpr (QC + 1 == MOE_GCH && C + 1 < NC) {
       uint32_t *nb = lds + ((C + 1) & 1) * MOE_GCH_BUF_DW;
       gstage_store<NO>(r.stg, nb, g, tid);
       lds_barrier();
-      load_bs32_chunk<NO>(r.b[0], nb, lane, dlo, 0);
+      load_bs32_chunk<NO>(r.b[0], nb, z, dlo, 0);
     }
-    gl_from<QL + 1, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, lane, dlo, upper, sb, acc);
+    gl_from<QL + 1, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, z, dlo, sb, acc);
   }
 }
 
@@ -1151,6 +1201,11 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
   load_wq32<1, 0>(r.w[2], ws, ao, 2);
   gstage_load<NO, 0>(r.stg, src, g);
   gstage_store<NO>(r.stg, lds, g, tid);
+  if (tid < 2 * 2 * MOE_GCH_STEPS) {  // the zero slots of both chunk buffers, never written by the staging
+    const int bf = tid / (2 * MOE_GCH_STEPS), o = (tid / MOE_GCH_STEPS) & 1, st = tid % MOE_GCH_STEPS;
+    reinterpret_cast<u32x4_t *>(lds + bf * MOE_GCH_BUF_DW)[o * MOE_GCH_OCT_U4 + st * 65 + 64] =
+        u32x4_t{0u, 0u, 0u, 0u};
+  }
   lds_barrier();
   const int n = lane & 31, gb = lane >> 5, t = n >> 2;
   const int dlo = t * 2 + (n & 1);
@@ -1159,8 +1214,9 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
   for (int o = 0; o < NO; o++)
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[o][0][e] = 0.0f;
-  load_bs32_chunk<NO>(r.b[0], lds, lane, dlo, 0);
-  gl_from<0, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, lane, dlo, lane_upper32(lane), lane_bscale32(lane), acc);
+  const zoff z = make_zoff(lane);
+  load_bs32_chunk<NO>(r.b[0], lds, z, dlo, 0);
+  gl_from<0, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, z, dlo, lane_bscale32(lane), acc);
   lds_barrier();  // every wave is done with the chunk buffers, which now hold the sums
   float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
