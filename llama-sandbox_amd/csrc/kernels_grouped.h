@@ -754,6 +754,30 @@ __device__ __forceinline__ void stage_octet_lds(const uint32_t *__restrict__ hs,
   }
 }
 
+// The same layout with a 16-byte zero slot after each step's 64 lanes
+// (stride 65), read by the operand half without data (bs32z).
+__host__ __device__ constexpr size_t octet_lds_bytes_z(int KB) {
+  return (size_t)(KB / 2) * 65 * 16 + (size_t)(KB / 2) * 16 * 4;
+}
+
+__device__ __forceinline__ void stage_octet_lds_z(const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+                                                  int row0, int nt, int KB, u32x4_t *bl, float *dl, int tid,
+                                                  int nthr) {
+  const u32x4_t *src = reinterpret_cast<const u32x4_t *>(hs + (size_t)row0 * KB * MOE_XSW);
+  const int n16 = 8 * KB * 4;  // 16-byte chunks of 8 rows
+#pragma unroll 4
+  for (int c = tid; c < n16; c += nthr) {
+    const int t = c / (4 * KB), w = c - t * 4 * KB, b = w >> 2, sub = w & 3;
+    const int L = 32 * (sub & 1) + 4 * t + 2 * (sub >> 1) + (b & 1);
+    bl[(b >> 1) * 65 + L] = t < nt ? src[c] : u32x4_t{0u, 0u, 0u, 0u};
+  }
+  for (int c = tid; c < KB / 2; c += nthr) bl[c * 65 + 64] = u32x4_t{0u, 0u, 0u, 0u};
+  for (int c = tid; c < 8 * KB; c += nthr) {
+    const int t = c / KB, b = c - t * KB;
+    dl[((b >> 1) * 8 + t) * 2 + (b & 1)] = t < nt ? hd[(size_t)(row0 + t) * KB + b] : 0.0f;
+  }
+}
+
 // Ring of the LDS-B octet loop: weights of 4 quads (3 ahead), B of 2 quads
 // (1 ahead, from LDS) for NO octets, exponent dwords of NG groups.
 template <int NW, int NO, int NG>
@@ -851,161 +875,6 @@ void k_down_ol(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   }
 }
 
-// B of one step (2 blocks) for NO octets, read from LDS one step ahead.
-template <int NO>
-struct bs32 {
-  u32x4_t v[NO];
-  float d[NO];
-};
-
-template <int NO, int OB, int OD>
-__device__ __forceinline__ void load_bs32_lds(bs32<NO> &b, const u32x4_t *bl, const float *dl, int lane, int dlo,
-                                              int step) {
-#pragma unroll
-  for (int o = 0; o < NO; o++) {
-    b.v[o] = bl[o * OB + step * 64 + lane];
-    b.d[o] = dl[o * OD + step * 16 + dlo];
-  }
-}
-
-// Step J of a quad (op_sel SEL = quad % 4): acc[o] += d[o] * (A . B[o]) for
-// one weight stream; the per-octet sequence is that of quad_mma32.
-template <int SEL, int J, int NO>
-__device__ __forceinline__ void step_mma32(const wq32<1> &w, const uint32_t (&sc)[1][2], const bs32<NO> &b,
-                                           bool upper, int sb, f32x16_t (&acc)[NO][1]) {
-  const u32x4_t a4 = w.w[0][J];
-  const i32x8_t a = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
-#pragma unroll
-  for (int o = 0; o < NO; o++) {
-    const u32x4_t v = b.v[o];
-    i32x8_t bv;
-    bv[0] = upper ? 0 : (int)v.x; bv[1] = upper ? 0 : (int)v.y; bv[2] = upper ? 0 : (int)v.z; bv[3] = upper ? 0 : (int)v.w;
-    bv[4] = upper ? (int)v.x : 0; bv[5] = upper ? (int)v.y : 0; bv[6] = upper ? (int)v.z : 0; bv[7] = upper ? (int)v.w : 0;
-    f32x16_t z;
-#pragma unroll
-    for (int e = 0; e < 16; e++) z[e] = 0.0f;
-    const f32x16_t r = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bv, z, 4, 0, SEL, (int)sc[0][J], 0, sb);
-    acc[o][0] = acc[o][0] + b.d[o] * r;
-  }
-#pragma unroll
-  for (int o = 0; o < NO; o++) asm volatile("" : "+v"(acc[o][0]));
-}
-
-// Ring of the step-B loop: weights of 4 quads (3 ahead) of one stream,
-// exponent dwords of NG groups, B of 2 steps.
-template <int NO, int NG>
-struct sring {
-  wq32<1> w[4];
-  uint32_t sc[NG][1][2];
-  bs32<NO> b[2];
-};
-
-// Quads QL .. NQW-1 with B from LDS one step ahead.
-template <int QL, int NQW, int NO, int NG, int OB, int OD>
-__device__ __forceinline__ void slfixed_from(sring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao,
-                                             const u32x4_t *bl, const float *dl, int lane, int dlo, bool upper,
-                                             int sb, f32x16_t (&acc)[NO][1]) {
-  if constexpr (QL < NQW) {
-    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
-    if constexpr (QL + 3 < NQW) load_wq32<1, 0>(r.w[(QL + 3) & 3], ws, ao, QL + 3);
-    load_bs32_lds<NO, OB, OD>(r.b[1], bl, dl, lane, dlo, 2 * QL + 1);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    step_mma32<QL & 3, 0, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[0], upper, sb, acc);
-    if constexpr (QL + 1 < NQW) load_bs32_lds<NO, OB, OD>(r.b[0], bl, dl, lane, dlo, 2 * QL + 2);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    step_mma32<QL & 3, 1, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[1], upper, sb, acc);
-    slfixed_from<QL + 1, NQW, NO, NG, OB, OD>(r, ws, ao, bl, dl, lane, dlo, upper, sb, acc);
-  }
-}
-
-#define MOE_DOL2_WAVES 8
-
-// The down work of one wave against NO octets staged at lds (octet o at
-// dword o * octet_lds_bytes(KB) / 4): y of token 8*o + t of the item.
-template <int NQ, int NO>
-__device__ __forceinline__ void dn_ol_octets(const wstream (&ws)[1], const aoff32 &ao, uint32_t *lds,
-                                             const uint32_t *__restrict__ hs, const float *__restrict__ hd,
-                                             const int4 &it, const int32_t *__restrict__ perm,
-                                             const float *__restrict__ wts, int H, int t32, int lane,
-                                             float *__restrict__ y) {
-  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, KB = NQ * 4;
-  constexpr int OW = (int)(octet_lds_bytes(KB) / 4);  // dwords per staged octet
-  const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
-  sring<NO, NG> r;
-  // first weights in flight during the staging
-  load_sc32<1>(r.sc[0], ws, ao, 0);
-  load_wq32<1, 0>(r.w[0], ws, ao, 0);
-  if (NQ > 1) load_wq32<1, 0>(r.w[1], ws, ao, 1);
-  if (NQ > 2) load_wq32<1, 0>(r.w[2], ws, ao, 2);
-#pragma unroll
-  for (int o = 0; o < NO; o++) {
-    uint32_t *ol = lds + o * OW;
-    stage_octet_lds(hs, hd, row0 + 8 * o, nt - 8 * o, KB, reinterpret_cast<u32x4_t *>(ol),
-                    reinterpret_cast<float *>(ol + (KB / 2) * 64 * 4), threadIdx.x, 64 * MOE_DOL2_WAVES);
-  }
-  __syncthreads();
-  const u32x4_t *bl = reinterpret_cast<const u32x4_t *>(lds);
-  const float *dl = reinterpret_cast<const float *>(lds + (KB / 2) * 64 * 4);
-  const int n = lane & 31, gb = lane >> 5, t = n >> 2;
-  const int dlo = t * 2 + (n & 1);
-  f32x16_t acc[NO][1];
-#pragma unroll
-  for (int o = 0; o < NO; o++)
-#pragma unroll
-    for (int e = 0; e < 16; e++) acc[o][0][e] = 0.0f;
-  load_bs32_lds<NO, OW / 4, OW>(r.b[0], bl, dl, lane, dlo, 0);
-  slfixed_from<0, NQ, NO, NG, OW / 4, OW>(r, ws, ao, bl, dl, lane, dlo, lane_upper32(lane), lane_bscale32(lane), acc);
-#pragma unroll
-  for (int o = 0; o < NO; o++) {
-    const int tt = 8 * o + t;
-    const bool live = tt < nt;
-    const int rr = row0 + (live ? tt : 0);
-    const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
-    float v[16];
-#pragma unroll
-    for (int e = 0; e < 16; e++) {
-      v[e] = col4_sum(acc[o][0][e]);
-      if (!shared) v[e] = __fmul_rn(v[e], wt);
-    }
-    if ((n & 3) == 0 && live) {
-      float *dst = y + (size_t)rr * H + (size_t)t32 * 32 + 4 * gb;
-#pragma unroll
-      for (int i = 0; i < 4; i++)
-        *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
-    }
-  }
-}
-
-// k_down_ol on items of up to 16 rows: a workgroup of 8 waves stages the
-// item's two octets of h in LDS (octet 1 only when the item holds more than
-// 8 rows) and each wave multiplies its 32-row tile of H against both from
-// the same weight registers, so one pass over the item's down weights
-// serves 16 tokens; B is read from LDS one step ahead, which keeps the wave
-// within 128 VGPRs (4 waves per SIMD with two workgroups per CU).  Per
-// token the MFMA and scaling sequence is k_down_ol's (same bits).
-// grid (H/256, item capacity), 512 threads, LDS 2 * octet_lds_bytes(F/32).
-template <int NQ>
-__global__ __launch_bounds__(64 * MOE_DOL2_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
-void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
-                int n_rows, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
-                const float *__restrict__ wts, int F, int H, float *__restrict__ y) {
-  extern __shared__ __align__(16) uint32_t lds[];
-  if ((int)blockIdx.y >= items[0]) return;
-  const int4 it = item_of(items, blockIdx.y);
-  constexpr int NQ4 = (NQ + 3) / 4;
-  const int tiles = H / MOE_TILE;
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int t32 = blockIdx.x * MOE_DOL2_WAVES + wave;  // 32-row tile of H
-  const int nt = it.z;
-  const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
-  const aoff32 ao = make_aoff32(lane, NQ4);
-  if (nt > 8) dn_ol_octets<NQ, 2>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);  // uniform branch
-  else dn_ol_octets<NQ, 1>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);
-}
-
 // B of one step as both 16-byte halves of each octet's MFMA operand, read
 // from LDS where each step's 64 lanes are followed by a 16-byte zero slot
 // (stride 65): the half that carries no data reads the zero slot, so the
@@ -1038,7 +907,8 @@ __device__ __forceinline__ void load_bs32z_lds(bs32z<NO> &b, const u32x4_t *bl, 
   }
 }
 
-// step_mma32 on a bs32z operand (same sequence, same bits).
+// Step J of a quad (op_sel SEL = quad % 4): acc[o] += d[o] * (A . B[o]) for
+// one weight stream; the per-octet sequence is that of quad_mma32 (same bits).
 template <int SEL, int J, int NO>
 __device__ __forceinline__ void step_mma32z(const wq32<1> &w, const uint32_t (&sc)[1][2], const bs32z<NO> &b, int sb,
                                             f32x16_t (&acc)[NO][1]) {
@@ -1056,6 +926,125 @@ __device__ __forceinline__ void step_mma32z(const wq32<1> &w, const uint32_t (&s
   }
 #pragma unroll
   for (int o = 0; o < NO; o++) asm volatile("" : "+v"(acc[o][0]));
+}
+
+// Ring of the step-B loop: weights of 3 quads (2 ahead) of one stream,
+// exponent dwords of NG groups, B of the next step (a zero-slot operand,
+// read from LDS right after the previous step's MFMAs are issued; a deeper
+// B ring does not fit 128 registers).
+template <int NO, int NG>
+struct sring {
+  wq32<1> w[3];
+  uint32_t sc[NG][1][2];
+  bs32z<NO> b[1];
+};
+
+// Quads QL .. NQW-1 with B from LDS one step ahead.
+template <int QL, int NQW, int NO, int NG, int OB, int OD>
+__device__ __forceinline__ void slfixed_from(sring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao,
+                                             const u32x4_t *bl, const float *dl, const zoff &z, int dlo, int sb,
+                                             f32x16_t (&acc)[NO][1]) {
+  if constexpr (QL < NQW) {
+    if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
+    if constexpr (QL + 2 < NQW) load_wq32<1, 0>(r.w[(QL + 2) % 3], ws, ao, QL + 2);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step_mma32z<QL & 3, 0, NO>(r.w[QL % 3], r.sc[QL >> 2], r.b[0], sb, acc);
+    load_bs32z_lds<NO, OB, OD>(r.b[0], bl, dl, z, dlo, 2 * QL + 1);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step_mma32z<QL & 3, 1, NO>(r.w[QL % 3], r.sc[QL >> 2], r.b[0], sb, acc);
+    if constexpr (QL + 1 < NQW) load_bs32z_lds<NO, OB, OD>(r.b[0], bl, dl, z, dlo, 2 * QL + 2);
+    slfixed_from<QL + 1, NQW, NO, NG, OB, OD>(r, ws, ao, bl, dl, z, dlo, sb, acc);
+  }
+}
+
+#define MOE_DOL2_WAVES 8
+
+// The down work of one wave against NO octets staged at lds (octet o at
+// dword o * octet_lds_bytes(KB) / 4): y of token 8*o + t of the item.
+template <int NQ, int NO>
+__device__ __forceinline__ void dn_ol_octets(const wstream (&ws)[1], const aoff32 &ao, uint32_t *lds,
+                                             const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+                                             const int4 &it, const int32_t *__restrict__ perm,
+                                             const float *__restrict__ wts, int H, int t32, int lane,
+                                             float *__restrict__ y) {
+  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, KB = NQ * 4;
+  constexpr int OW = (int)(octet_lds_bytes_z(KB) / 4);  // dwords per staged octet
+  const int row0 = it.y, nt = it.z;
+  const bool shared = it.w != 0;
+  sring<NO, NG> r;
+  // first weights in flight during the staging
+  load_sc32<1>(r.sc[0], ws, ao, 0);
+  load_wq32<1, 0>(r.w[0], ws, ao, 0);
+  if (NQ > 1) load_wq32<1, 0>(r.w[1], ws, ao, 1);
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    uint32_t *ol = lds + o * OW;
+    stage_octet_lds_z(hs, hd, row0 + 8 * o, nt - 8 * o, KB, reinterpret_cast<u32x4_t *>(ol),
+                      reinterpret_cast<float *>(ol + (KB / 2) * 65 * 4), threadIdx.x, 64 * MOE_DOL2_WAVES);
+  }
+  __syncthreads();
+  const u32x4_t *bl = reinterpret_cast<const u32x4_t *>(lds);
+  const float *dl = reinterpret_cast<const float *>(lds + (KB / 2) * 65 * 4);
+  const int n = lane & 31, gb = lane >> 5, t = n >> 2;
+  const int dlo = t * 2 + (n & 1);
+  f32x16_t acc[NO][1];
+#pragma unroll
+  for (int o = 0; o < NO; o++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[o][0][e] = 0.0f;
+  const zoff z = make_zoff(lane);
+  load_bs32z_lds<NO, OW / 4, OW>(r.b[0], bl, dl, z, dlo, 0);
+  slfixed_from<0, NQ, NO, NG, OW / 4, OW>(r, ws, ao, bl, dl, z, dlo, lane_bscale32(lane), acc);
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    const int tt = 8 * o + t;
+    const bool live = tt < nt;
+    const int rr = row0 + (live ? tt : 0);
+    const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
+    float v[16];
+#pragma unroll
+    for (int e = 0; e < 16; e++) {
+      v[e] = col4_sum(acc[o][0][e]);
+      if (!shared) v[e] = __fmul_rn(v[e], wt);
+    }
+    if ((n & 3) == 0 && live) {
+      float *dst = y + (size_t)rr * H + (size_t)t32 * 32 + 4 * gb;
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+        *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    }
+  }
+}
+
+// k_down_ol on items of up to 16 rows: a workgroup of 8 waves stages the
+// item's two octets of h in LDS (octet 1 only when the item holds more than
+// 8 rows) and each wave multiplies its 32-row tile of H against both from
+// the same weight registers, so one pass over the item's down weights
+// serves 16 tokens.  Both halves of each block-diagonal B operand come from
+// LDS (the half without data from the step's zero slot: no selects), one
+// step ahead, which keeps the wave within 128 VGPRs (4 waves per SIMD with
+// two workgroups per CU).  Per token the MFMA and scaling sequence is
+// k_down_ol's (same bits).  grid (H/256, item capacity), 512 threads, LDS
+// 2 * octet_lds_bytes_z(F/32).
+template <int NQ>
+__global__ __launch_bounds__(64 * MOE_DOL2_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
+void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
+                int n_rows, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
+                const float *__restrict__ wts, int F, int H, float *__restrict__ y) {
+  extern __shared__ __align__(16) uint32_t lds[];
+  if ((int)blockIdx.y >= items[0]) return;
+  const int4 it = item_of(items, blockIdx.y);
+  constexpr int NQ4 = (NQ + 3) / 4;
+  const int tiles = H / MOE_TILE;
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int t32 = blockIdx.x * MOE_DOL2_WAVES + wave;  // 32-row tile of H
+  const int nt = it.z;
+  const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
+  const aoff32 ao = make_aoff32(lane, NQ4);
+  if (nt > 8) dn_ol_octets<NQ, 2>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);  // uniform branch
+  else dn_ol_octets<NQ, 1>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);
 }
 
 // ===========================================================================

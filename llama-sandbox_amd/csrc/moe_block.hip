@@ -401,7 +401,7 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
                                                   {(const void *)k_down_ol2<6>, 6 * 4}};
   for (const auto &kb : big_lds)
     if (hipFuncSetAttribute(kb.first, hipFuncAttributeMaxDynamicSharedMemorySize,
-                            (int)(2 * octet_lds_bytes(kb.second))) != hipSuccess) {
+                            (int)(2 * octet_lds_bytes_z(kb.second))) != hipSuccess) {
       delete c;
       return MOE_ERR_NO_DEVICE;
     }
@@ -890,16 +890,16 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     prof_scope pd(c, K_DOWN_GROUPED, st, s.timed);
 #define MOE_DN_ARGS L.m[T_DOWN].w, s.hq, s.hd, P + T, items, perm, wts, F, H, s.y
     const dim3 gdo(H / 128, cap);
-    const size_t lo = octet_lds_bytes(F / MOE_QK);
+    const size_t lo = octet_lds_bytes(F / MOE_QK), lo2 = 2 * octet_lds_bytes_z(F / MOE_QK);
     // two octets per wave on the 16-row items where that list exists and two
     // workgroups' LDS (2 x 2 staged octets) fit a CU
     const dim3 gdo2(H / (32 * MOE_DOL2_WAVES), group_item_cap(T, k, E, 16));
     const bool dn2 = o2 && H % (32 * MOE_DOL2_WAVES) == 0;
     const dim3 b2(64 * MOE_DOL2_WAVES);
 #define MOE_DN_ARGS16 L.m[T_DOWN].w, s.hq, s.hd, P + T, items16, perm, wts, F, H, s.y
-    if (dn2 && F == 128 * 16) hipLaunchKernelGGL(k_down_ol2<16>, gdo2, b2, 2 * lo, st, MOE_DN_ARGS16);
-    else if (dn2 && F == 128 * 8) hipLaunchKernelGGL(k_down_ol2<8>, gdo2, b2, 2 * lo, st, MOE_DN_ARGS16);
-    else if (dn2 && F == 128 * 6) hipLaunchKernelGGL(k_down_ol2<6>, gdo2, b2, 2 * lo, st, MOE_DN_ARGS16);
+    if (dn2 && F == 128 * 16) hipLaunchKernelGGL(k_down_ol2<16>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
+    else if (dn2 && F == 128 * 8) hipLaunchKernelGGL(k_down_ol2<8>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
+    else if (dn2 && F == 128 * 6) hipLaunchKernelGGL(k_down_ol2<6>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (oct && F == 128 * 16) hipLaunchKernelGGL(k_down_ol<16>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
     else if (oct && F == 128 * 6) hipLaunchKernelGGL(k_down_ol<6>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
     else if (oct && F == 128 * 8) hipLaunchKernelGGL(k_down_ol<8>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
