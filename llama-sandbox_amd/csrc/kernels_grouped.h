@@ -1056,13 +1056,14 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 // B (the octets' x rows) into LDS in chunks of MOE_GCH quads, already in
 // MFMA lane order (the layout of stage_octet_lds, per chunk, each step's 64
 // lanes followed by a 16-byte zero slot), double buffered: the global loads
-// of chunk c+1 are issued as chunk c starts and written to the other buffer
-// as it ends, then one barrier.  Every B byte thus crosses the vector-memory
-// unit once per workgroup; the waves read both halves of each MFMA operand
-// from LDS one step ahead (the half without data from the zero slot, so no
-// selects), and a wave's registers hold one weight stream (3 waves per
-// SIMD).  After the K loop gate and up meet in LDS for clamp + SwiGLU +
-// Q8_0(h) as in k_gate_up_o.
+// of chunk c+1 are issued in two halves during chunk c and written to the
+// other buffer one quad later, then one barrier at its end.  Every B byte
+// thus crosses the vector-memory unit once per workgroup; a wave reads both
+// halves of each MFMA operand from LDS (the half without data from the zero
+// slot, so no selects) right after the previous step's MFMAs, and holds one
+// weight stream with a ring of 2 quads: 122 VGPRs, 4 waves per SIMD, which
+// beat deeper rings at 3 waves.  After the K loop gate and up meet in LDS
+// for clamp + SwiGLU + Q8_0(h) as in k_gate_up_o.
 #define MOE_GCH 4                                  // quads per staged chunk
 #define MOE_GCH_STEPS (2 * MOE_GCH)                // MFMA steps per chunk
 #define MOE_GCH_OCT_U4 (MOE_GCH_STEPS * 65)        // 16-byte units per octet per chunk (digits, zero slots)
@@ -1083,6 +1084,13 @@ struct gstage {
 template <int NO>
 struct gstage_regs {
   u32x4_t v[2 * NO];
+  float d;
+};
+
+// Half P of a chunk's staging (pieces m = 2P, 2P+1; the scales with the last
+// half), carried in registers from its loads to its LDS stores.
+struct gstage_half {
+  u32x4_t v[2];
   float d;
 };
 
@@ -1111,6 +1119,24 @@ __device__ __forceinline__ void gstage_load(gstage_regs<NO> &s, const gsrc &src,
   s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
 }
 
+template <int NO, int C, int P>
+__device__ __forceinline__ void gstage_load_half(gstage_half &s, const gsrc &src, const gstage<NO> &g) {
+#pragma unroll
+  for (int i = 0; i < 2; i++)
+    s.v[i] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[2 * P + i], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
+  if constexpr (P == NO - 1)
+    s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
+}
+
+template <int NO, int P>
+__device__ __forceinline__ void gstage_store_half(const gstage_half &s, uint32_t *buf, const gstage<NO> &g, int tid) {
+  u32x4_t *bu = reinterpret_cast<u32x4_t *>(buf);
+#pragma unroll
+  for (int i = 0; i < 2; i++) bu[g.lu4[2 * P + i]] = s.v[i];
+  if constexpr (P == NO - 1)
+    if (NO == 2 || tid < 128) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // NO == 1: tokens < 8 only
+}
+
 template <int NO>
 __device__ __forceinline__ void gstage_store(const gstage_regs<NO> &s, uint32_t *buf, const gstage<NO> &g,
                                              int tid) {
@@ -1136,10 +1162,10 @@ __device__ __forceinline__ void load_bs32_chunk(bs32z<NO> &b, const uint32_t *bu
 
 template <int NO, int NG>
 struct gring {
-  wq32<1> w[4];
+  wq32<1> w[2];
   uint32_t sc[NG][1][2];
-  bs32z<NO> b[2];
-  gstage_regs<NO> stg;
+  bs32z<NO> b[1];
+  gstage_half stg;
 };
 
 // Quads QL .. NQ-1 of the chunked K loop.
@@ -1150,20 +1176,23 @@ __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1]
   if constexpr (QL < NQ) {
     constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH;
     const uint32_t *buf = lds + (C & 1) * MOE_GCH_BUF_DW;
-    if constexpr (QC == 0 && C + 1 < NC) gstage_load<NO, C + 1>(r.stg, src, g);
+    // the next chunk's staging in halves: loads at quads 0 and 2 of this
+    // chunk, LDS stores at the ends of quads 1 and 3
+    if constexpr (C + 1 < NC && (QC == 0 || (QC == 2 && NO == 2))) gstage_load_half<NO, C + 1, QC / 2>(r.stg, src, g);
     if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
-    if constexpr (QL + 3 < NQ) load_wq32<1, 0>(r.w[(QL + 3) & 3], ws, ao, QL + 3);
-    load_bs32_chunk<NO>(r.b[1], buf, z, dlo, 2 * QC + 1);
+    if constexpr (QL + 1 < NQ) load_wq32<1, 0>(r.w[(QL + 1) & 1], ws, ao, QL + 1);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32z<QL & 3, 0, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[0], sb, acc);
+    step_mma32z<QL & 3, 0, NO>(r.w[QL & 1], r.sc[QL >> 2], r.b[0], sb, acc);
+    load_bs32_chunk<NO>(r.b[0], buf, z, dlo, 2 * QC + 1);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    step_mma32z<QL & 3, 1, NO>(r.w[QL & 1], r.sc[QL >> 2], r.b[0], sb, acc);
     if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk<NO>(r.b[0], buf, z, dlo, 2 * QC + 2);
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    step_mma32z<QL & 3, 1, NO>(r.w[QL & 3], r.sc[QL >> 2], r.b[1], sb, acc);
+    if constexpr (C + 1 < NC && (QC == 1 || (QC == 3 && NO == 2)))
+      gstage_store_half<NO, QC / 2>(r.stg, lds + ((C + 1) & 1) * MOE_GCH_BUF_DW, g, tid);
     if constexpr (QC + 1 == MOE_GCH && C + 1 < NC) {
       uint32_t *nb = lds + ((C + 1) & 1) * MOE_GCH_BUF_DW;
-      gstage_store<NO>(r.stg, nb, g, tid);
       lds_barrier();
       load_bs32_chunk<NO>(r.b[0], nb, z, dlo, 0);
     }
@@ -1186,10 +1215,11 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
   // first weights in flight during the first staging
   load_sc32<1>(r.sc[0], ws, ao, 0);
   load_wq32<1, 0>(r.w[0], ws, ao, 0);
-  load_wq32<1, 0>(r.w[1], ws, ao, 1);
-  load_wq32<1, 0>(r.w[2], ws, ao, 2);
-  gstage_load<NO, 0>(r.stg, src, g);
-  gstage_store<NO>(r.stg, lds, g, tid);
+  {
+    gstage_regs<NO> s0;  // chunk 0 in one go: nothing else is in the ring yet
+    gstage_load<NO, 0>(s0, src, g);
+    gstage_store<NO>(s0, lds, g, tid);
+  }
   if (tid < 2 * 2 * MOE_GCH_STEPS) {  // the zero slots of both chunk buffers, never written by the staging
     const int bf = tid / (2 * MOE_GCH_STEPS), o = (tid / MOE_GCH_STEPS) & 1, st = tid % MOE_GCH_STEPS;
     reinterpret_cast<u32x4_t *>(lds + bf * MOE_GCH_BUF_DW)[o * MOE_GCH_OCT_U4 + st * 65 + 64] =
@@ -1221,7 +1251,7 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
 // grid (F/64, item capacity), 256 threads, LDS 2 * MOE_GCH_BUF_DW dwords.
 // Requires H == 128 * NQ, NQ % MOE_GCH == 0.
 template <int NQ>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
 void k_gate_up_ol(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
                   const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                   int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
