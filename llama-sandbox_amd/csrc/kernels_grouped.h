@@ -1050,9 +1050,9 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 // ===========================================================================
 // Grouped gate/up with the item's B staged in LDS, chunk by chunk of K.
 //
-// One workgroup of 4 waves per (2 units of F, item of <= 16 rows): wave w
-// streams the gate (w < 2) or up (w >= 2) tile of unit 2*blockIdx.x + w%2
-// over all of K against the item's one or two octets.  The workgroup copies
+// One workgroup of 2*NU waves per (NU units of F, item of <= 16 rows): wave
+// w streams the gate (w < NU) or up tile of unit NU*blockIdx.x + w%NU over
+// all of K against the item's one or two octets.  The workgroup copies
 // B (the octets' x rows) into LDS in chunks of MOE_GCH quads, already in
 // MFMA lane order (the layout of stage_octet_lds, per chunk, each step's 64
 // lanes followed by a 16-byte zero slot), double buffered: the global loads
@@ -1070,37 +1070,40 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 #define MOE_GCH_OCT_D (MOE_GCH_STEPS * 16)         // scales per octet per chunk
 #define MOE_GCH_BUF_DW (2 * MOE_GCH_OCT_U4 * 4 + 2 * MOE_GCH_OCT_D)  // dwords per chunk buffer (two octets)
 
-// This thread's part of the staging: 16-byte digit pieces of tokens
-// t = tid/64 + 4m (m < 2*NO) at block b = (tid%64)/4, piece sub = tid%4 of
-// each chunk, and the scale of token tid/16, block tid%16.
-template <int NO>
+// This thread's part of the staging, for a workgroup of 128*NU threads:
+// PT = 4*NO/NU 16-byte digit pieces of tokens t = tid/64 + 2*NU*m (m < PT)
+// at block b = (tid%64)/4, piece sub = tid%4 of each chunk, and (tid <
+// 128*NO) the scale of token tid/16, block tid%16.
+template <int NO, int NU>
 struct gstage {
-  uint32_t xo[2 * NO];  // byte offset in the digit rows at chunk 0 (MOE_OOB: absent token)
-  int lu4[2 * NO];      // 16-byte unit in the chunk buffer
-  uint32_t dof;         // byte offset in the scale rows at chunk 0
-  int ld;               // float index in the chunk buffer
+  static constexpr int PT = 4 * NO / NU;  // pieces per thread and chunk
+  uint32_t xo[PT];                        // byte offset in the digit rows at chunk 0 (MOE_OOB: absent token)
+  int lu4[PT];                            // 16-byte unit in the chunk buffer
+  uint32_t dof;                           // byte offset in the scale rows at chunk 0
+  int ld;                                 // float index in the chunk buffer
 };
 
-template <int NO>
+template <int NO, int NU>
 struct gstage_regs {
-  u32x4_t v[2 * NO];
+  u32x4_t v[4 * NO / NU];
   float d;
 };
 
-// Half P of a chunk's staging (pieces m = 2P, 2P+1; the scales with the last
-// half), carried in registers from its loads to its LDS stores.
+// Half P of a chunk's staging (pieces m = 2P, 2P+1, or the one piece when a
+// thread has one; the scales with the last half), carried in registers from
+// its loads to its LDS stores.
 struct gstage_half {
   u32x4_t v[2];
   float d;
 };
 
-template <int NO>
-__device__ __forceinline__ gstage<NO> make_gstage(int tid, const int (&xr)[2 * NO], int xr_d, int KB) {
-  gstage<NO> g;
+template <int NO, int NU>
+__device__ __forceinline__ gstage<NO, NU> make_gstage(int tid, const int (&xr)[4 * NO / NU], int xr_d, int KB) {
+  gstage<NO, NU> g;
   const int w = tid & 63, b = w >> 2, sub = w & 3;
 #pragma unroll
-  for (int m = 0; m < 2 * NO; m++) {
-    const int t = (tid >> 6) + 4 * m, o = t >> 3, tt = t & 7;
+  for (int m = 0; m < gstage<NO, NU>::PT; m++) {
+    const int t = (tid >> 6) + 2 * NU * m, o = t >> 3, tt = t & 7;
     g.xo[m] = xr[m] >= 0 ? (uint32_t)((xr[m] * KB + b) * (MOE_XSW * 4) + sub * 16) : MOE_OOB;
     g.lu4[m] = o * MOE_GCH_OCT_U4 + (b >> 1) * 65 + 32 * (sub & 1) + 4 * tt + 2 * (sub >> 1) + (b & 1);
   }
@@ -1111,39 +1114,48 @@ __device__ __forceinline__ gstage<NO> make_gstage(int tid, const int (&xr)[2 * N
 }
 
 // Global loads of chunk C (blocks 16*C .. 16*C + 15 of every row).
-template <int NO, int C>
-__device__ __forceinline__ void gstage_load(gstage_regs<NO> &s, const gsrc &src, const gstage<NO> &g) {
+template <int NO, int NU, int C>
+__device__ __forceinline__ void gstage_load(gstage_regs<NO, NU> &s, const gsrc &src, const gstage<NO, NU> &g) {
 #pragma unroll
-  for (int m = 0; m < 2 * NO; m++)
+  for (int m = 0; m < gstage<NO, NU>::PT; m++)
     s.v[m] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[m], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
   s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
 }
 
-template <int NO, int C, int P>
-__device__ __forceinline__ void gstage_load_half(gstage_half &s, const gsrc &src, const gstage<NO> &g) {
+// The staging of one chunk in halves of up to 2 pieces.
+template <int NO, int NU>
+struct ghalves {
+  static constexpr int PT = gstage<NO, NU>::PT, HS = PT < 2 ? PT : 2, NH = PT / HS;
+};
+
+template <int NO, int NU, int C, int P>
+__device__ __forceinline__ void gstage_load_half(gstage_half &s, const gsrc &src, const gstage<NO, NU> &g) {
+  constexpr int HS = ghalves<NO, NU>::HS, NH = ghalves<NO, NU>::NH;
 #pragma unroll
-  for (int i = 0; i < 2; i++)
-    s.v[i] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[2 * P + i], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
-  if constexpr (P == NO - 1)
+  for (int i = 0; i < HS; i++)
+    s.v[i] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[HS * P + i], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
+  if constexpr (P == NH - 1)
     s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
 }
 
-template <int NO, int P>
-__device__ __forceinline__ void gstage_store_half(const gstage_half &s, uint32_t *buf, const gstage<NO> &g, int tid) {
+template <int NO, int NU, int P>
+__device__ __forceinline__ void gstage_store_half(const gstage_half &s, uint32_t *buf, const gstage<NO, NU> &g,
+                                                  int tid) {
+  constexpr int HS = ghalves<NO, NU>::HS, NH = ghalves<NO, NU>::NH;
   u32x4_t *bu = reinterpret_cast<u32x4_t *>(buf);
 #pragma unroll
-  for (int i = 0; i < 2; i++) bu[g.lu4[2 * P + i]] = s.v[i];
-  if constexpr (P == NO - 1)
-    if (NO == 2 || tid < 128) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // NO == 1: tokens < 8 only
+  for (int i = 0; i < HS; i++) bu[g.lu4[HS * P + i]] = s.v[i];
+  if constexpr (P == NH - 1)
+    if (tid < 128 * NO) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // the scales of the present octets
 }
 
-template <int NO>
-__device__ __forceinline__ void gstage_store(const gstage_regs<NO> &s, uint32_t *buf, const gstage<NO> &g,
+template <int NO, int NU>
+__device__ __forceinline__ void gstage_store(const gstage_regs<NO, NU> &s, uint32_t *buf, const gstage<NO, NU> &g,
                                              int tid) {
   u32x4_t *bu = reinterpret_cast<u32x4_t *>(buf);
 #pragma unroll
-  for (int m = 0; m < 2 * NO; m++) bu[g.lu4[m]] = s.v[m];
-  if (NO == 2 || tid < 128) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // NO == 1: tokens < 8 only
+  for (int m = 0; m < gstage<NO, NU>::PT; m++) bu[g.lu4[m]] = s.v[m];
+  if (tid < 128 * NO) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // the scales of the present octets
 }
 
 // LDS writes of this wave done, then the workgroup barrier.
@@ -1169,16 +1181,18 @@ struct gring {
 };
 
 // Quads QL .. NQ-1 of the chunked K loop.
-template <int QL, int NQ, int NO, int NG>
+template <int QL, int NQ, int NO, int NU, int NG>
 __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
-                                        const gstage<NO> &g, uint32_t *lds, int tid, const zoff &z, int dlo, int sb,
-                                        f32x16_t (&acc)[NO][1]) {
+                                        const gstage<NO, NU> &g, uint32_t *lds, int tid, const zoff &z, int dlo,
+                                        int sb, f32x16_t (&acc)[NO][1]) {
   if constexpr (QL < NQ) {
     constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH;
     const uint32_t *buf = lds + (C & 1) * MOE_GCH_BUF_DW;
     // the next chunk's staging in halves: loads at quads 0 and 2 of this
     // chunk, LDS stores at the ends of quads 1 and 3
-    if constexpr (C + 1 < NC && (QC == 0 || (QC == 2 && NO == 2))) gstage_load_half<NO, C + 1, QC / 2>(r.stg, src, g);
+    constexpr int NH = ghalves<NO, NU>::NH;
+    if constexpr (C + 1 < NC && (QC & 1) == 0 && QC / 2 < NH)
+      gstage_load_half<NO, NU, C + 1, QC / 2>(r.stg, src, g);
     if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
     if constexpr (QL + 1 < NQ) load_wq32<1, 0>(r.w[(QL + 1) & 1], ws, ao, QL + 1);
     asm volatile("" ::: "memory");
@@ -1189,36 +1203,36 @@ __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1]
     __builtin_amdgcn_sched_barrier(0);
     step_mma32z<QL & 3, 1, NO>(r.w[QL & 1], r.sc[QL >> 2], r.b[0], sb, acc);
     if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk<NO>(r.b[0], buf, z, dlo, 2 * QC + 2);
-    if constexpr (C + 1 < NC && (QC == 1 || (QC == 3 && NO == 2)))
-      gstage_store_half<NO, QC / 2>(r.stg, lds + ((C + 1) & 1) * MOE_GCH_BUF_DW, g, tid);
+    if constexpr (C + 1 < NC && (QC & 1) == 1 && QC / 2 < NH)
+      gstage_store_half<NO, NU, QC / 2>(r.stg, lds + ((C + 1) & 1) * MOE_GCH_BUF_DW, g, tid);
     if constexpr (QC + 1 == MOE_GCH && C + 1 < NC) {
       uint32_t *nb = lds + ((C + 1) & 1) * MOE_GCH_BUF_DW;
       lds_barrier();
       load_bs32_chunk<NO>(r.b[0], nb, z, dlo, 0);
     }
-    gl_from<QL + 1, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, z, dlo, sb, acc);
+    gl_from<QL + 1, NQ, NO, NU, NG>(r, ws, ao, src, g, lds, tid, z, dlo, sb, acc);
   }
 }
 
-// The K loop of one wave against NO octets; leaves this wave's sums (the
-// 4 columns of a token added) in red[w%2][w/2][token][row].
-template <int NQ, int NO>
+// The K loop of one wave (of 2*NU) against NO octets; leaves this wave's
+// sums (the 4 columns of a token added) in red[w%NU][w/NU][token][row].
+template <int NQ, int NO, int NU>
 __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
-                                             const int (&xr)[4], int xr_d, int KB, uint32_t *lds, int tid,
+                                             const int (&xr)[8 / NU], int xr_d, int KB, uint32_t *lds, int tid,
                                              int wave, int lane) {
-  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4;
-  int xrm[2 * NO];
+  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, PT = gstage<NO, NU>::PT;
+  int xrm[PT];
 #pragma unroll
-  for (int m = 0; m < 2 * NO; m++) xrm[m] = xr[m];
-  const gstage<NO> g = make_gstage<NO>(tid, xrm, xr_d, KB);
+  for (int m = 0; m < PT; m++) xrm[m] = xr[m];
+  const gstage<NO, NU> g = make_gstage<NO, NU>(tid, xrm, xr_d, KB);
   gring<NO, NG> r;
   // first weights in flight during the first staging
   load_sc32<1>(r.sc[0], ws, ao, 0);
   load_wq32<1, 0>(r.w[0], ws, ao, 0);
   {
-    gstage_regs<NO> s0;  // chunk 0 in one go: nothing else is in the ring yet
-    gstage_load<NO, 0>(s0, src, g);
-    gstage_store<NO>(s0, lds, g, tid);
+    gstage_regs<NO, NU> s0;  // chunk 0 in one go: nothing else is in the ring yet
+    gstage_load<NO, NU, 0>(s0, src, g);
+    gstage_store<NO, NU>(s0, lds, g, tid);
   }
   if (tid < 2 * 2 * MOE_GCH_STEPS) {  // the zero slots of both chunk buffers, never written by the staging
     const int bf = tid / (2 * MOE_GCH_STEPS), o = (tid / MOE_GCH_STEPS) & 1, st = tid % MOE_GCH_STEPS;
@@ -1235,7 +1249,7 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
     for (int e = 0; e < 16; e++) acc[o][0][e] = 0.0f;
   const zoff z = make_zoff(lane);
   load_bs32_chunk<NO>(r.b[0], lds, z, dlo, 0);
-  gl_from<0, NQ, NO, NG>(r, ws, ao, src, g, lds, tid, z, dlo, lane_bscale32(lane), acc);
+  gl_from<0, NQ, NO, NU, NG>(r, ws, ao, src, g, lds, tid, z, dlo, lane_bscale32(lane), acc);
   lds_barrier();  // every wave is done with the chunk buffers, which now hold the sums
   float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
@@ -1244,14 +1258,18 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
     for (int e = 0; e < 16; e++) {
       const float v = col4_sum(acc[o][0][e]);
       if ((n & 3) == 0)
-        red[(((wave & 1) * 2 + (wave >> 1)) * 16 + 8 * o + (n >> 2)) * MOE_UNIT + 8 * (e >> 2) + 4 * gb + (e & 3)] = v;
+        red[(((wave % NU) * 2 + wave / NU) * 16 + 8 * o + (n >> 2)) * MOE_UNIT + 8 * (e >> 2) + 4 * gb + (e & 3)] = v;
     }
 }
 
-// grid (F/64, item capacity), 256 threads, LDS 2 * MOE_GCH_BUF_DW dwords.
-// Requires H == 128 * NQ, NQ % MOE_GCH == 0.
-template <int NQ>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+// grid (F/(32 NU), item capacity), 128*NU threads (NU units of F: wave w
+// streams the gate (w < NU) or up tile of unit NU*blockIdx.x + w%NU), LDS
+// 2 * MOE_GCH_BUF_DW dwords.  With NU = 4 the item's staged x serves twice
+// the weight rows of NU = 2, so the x rows are a fifth of the bytes a
+// workgroup moves instead of a third.  Requires H == 128 * NQ,
+// NQ % MOE_GCH == 0, (F/32) % NU == 0.
+template <int NQ, int NU>
+__global__ __launch_bounds__(128 * NU) __attribute__((amdgpu_waves_per_eu(4)))
 void k_gate_up_ol(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
                   const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                   int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
@@ -1264,30 +1282,30 @@ void k_gate_up_ol(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int P = T * k, row0 = it.y, nt = it.z;
   const bool shared = it.w != 0;
-  const int u = 2 * blockIdx.x + (wave & 1);
-  const wstream ws[1] = {make_wstream32((wave >> 1) ? w_u : w_g, (size_t)it.x * tiles + 2 * u, NQ4)};
+  const int u = NU * blockIdx.x + wave % NU;
+  const wstream ws[1] = {make_wstream32(wave >= NU ? w_u : w_g, (size_t)it.x * tiles + 2 * u, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
   const gsrc src = make_gsrc(xq, xd, T, KB);
   auto xrow = [&](int i) { return i < nt ? (shared ? row0 + i - P : perm[row0 + i] / k) : -1; };
-  int xr[4];
+  int xr[8 / NU];
 #pragma unroll
-  for (int m = 0; m < 4; m++) xr[m] = xrow((tid >> 6) + 4 * m);
-  const int xr_d = xrow(tid >> 4);
-  if (nt > 8) gu_ol_octets<NQ, 2>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);  // uniform branch
-  else gu_ol_octets<NQ, 1>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);
+  for (int m = 0; m < 8 / NU; m++) xr[m] = xrow((tid >> 6) + 2 * NU * m);
+  const int xr_d = tid < 256 ? xrow(tid >> 4) : -1;
+  if (nt > 8) gu_ol_octets<NQ, 2, NU>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);  // uniform branch
+  else gu_ol_octets<NQ, 1, NU>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);
   __syncthreads();
   const float *red = reinterpret_cast<const float *>(lds);
-  // (unit, token) c = 8*round + 2*wave + half-wave: unit c / 16, token c % 16
+  // (unit, token) c = 4*NU*round + 2*wave + half-wave: unit c / 16, token c % 16
 #pragma unroll
   for (int round = 0; round < 4; round++) {
-    if (8 * (round & 1) >= nt) continue;  // no token of this round is present (uniform over the workgroup)
-    const int c = 8 * round + 2 * wave + (lane >> 5);
+    const int c = 4 * NU * round + 2 * wave + (lane >> 5);
     const int ul2 = c >> 4, t = c & 15, j = lane & 31;
+    if (((4 * NU * round) & 15) >= nt && NU == 2) continue;  // no token of this round (uniform over the workgroup)
     const bool live = t < nt;
     const float gsum = red[((ul2 * 2 + 0) * 16 + t) * MOE_UNIT + j];
     const float usum = red[((ul2 * 2 + 1) * 16 + t) * MOE_UNIT + j];
     const float h = live ? swiglu(gsum, usum, clamp) : 0.0f;
-    const int hrow = row0 + (live ? t : 0), uu = 2 * blockIdx.x + ul2;
+    const int hrow = row0 + (live ? t : 0), uu = NU * blockIdx.x + ul2;
     h_unit_store(h, live, hs + ((size_t)hrow * U + uu) * MOE_XSW, hd + (size_t)hrow * U + uu, lane);
     if (htap && live) htap[(size_t)hrow * F + (size_t)uu * MOE_UNIT + j] = h;
   }

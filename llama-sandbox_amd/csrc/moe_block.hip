@@ -860,7 +860,7 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
   // a second list of items of up to 16 rows, B staged in LDS; below that most
   // items hold one octet and the 8-row list with B from global memory is used
   int32_t *items16 = items + group_list_words(T, k, E);
-  const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 2 == 0 &&
+  const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 4 == 0 &&
                   (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
@@ -875,10 +875,10 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     prof_scope pg(c, K_GU_GROUPED, st, s.timed);
 #define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
 #define MOE_GU_ARGS16 L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items16, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
-    const dim3 g16(F / (2 * MOE_UNIT), group_item_cap(T, k, E, 16));
-    if (o2 && H == 128 * 56) hipLaunchKernelGGL(k_gate_up_ol<56>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
-    else if (o2 && H == 128 * 32) hipLaunchKernelGGL(k_gate_up_ol<32>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
-    else if (o2 && H == 128 * 16) hipLaunchKernelGGL(k_gate_up_ol<16>, g16, dim3(256), 0, st, MOE_GU_ARGS16);
+    const dim3 g16(F / (4 * MOE_UNIT), group_item_cap(T, k, E, 16));  // 4 units of F per workgroup
+    if (o2 && H == 128 * 56) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<56, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
+    else if (o2 && H == 128 * 32) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<32, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
+    else if (o2 && H == 128 * 16) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<16, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
     else if (oct) hipLaunchKernelGGL(k_gate_up_o, dim3(F / (2 * MOE_UNIT), cap), dim3(256), 0, st, MOE_GU_ARGS);
     else hipLaunchKernelGGL(k_gate_up_g<2>, dim3(F / MOE_UNIT, cap), dim3(256), 0, st, MOE_GU_ARGS);
 #undef MOE_GU_ARGS
