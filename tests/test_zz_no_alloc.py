@@ -45,6 +45,7 @@ def _pair(ctx, oracle, layer, shape, T, seed, flags=0):
     (0, (16, 1), 0),                       # V3 grouped, then decode (bal2 gate/up tickets)
     (0, (1, 1), mb.MOE_FWD_NO_SHARED),     # V3 decode without shared: every unit met by a ticket
     (1, (9, 2), mb.MOE_FWD_PER_SLOT),      # C1 grouped per-slot
+    (1, (40, 20), 0),                      # C1 on the 16-row items (k_gate_up_ol, k_down_ol2)
     (1, (1, 1), 0),                        # C1 decode
 ])
 def test_noalloc_equals_forward(ctx, oracle, layer, Ts, flags):
