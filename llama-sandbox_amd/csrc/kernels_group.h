@@ -238,6 +238,27 @@ __global__ __launch_bounds__(256) void k_combine4(const float *__restrict__ y,
     }
     return;
   }
+  if (H4 % 256 == 0 && k <= 16 && inv) {
+    // one token per workgroup: its k grouped rows read first (uniform) and
+    // every row's float4 loaded before the sum (same order, same bits)
+    const int tu = __builtin_amdgcn_readfirstlane(t);
+    int r[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++)
+      if (s < k) r[s] = __builtin_amdgcn_readfirstlane(inv[tu * k + s]);
+    float4 v[16];
+#pragma unroll
+    for (int s = 0; s < 16; s++)
+      if (s < k) v[s] = r[s] >= 0 ? y4[(size_t)r[s] * H4 + c] : z;
+    const float4 vs = shared ? y4[((size_t)P + tu) * H4 + c] : z;
+    float4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < 16; s++)
+      if (s < k) acc = add4_rn(acc, v[s]);
+    if (shared) acc = add4_rn(acc, vs);
+    o4[i] = acc;
+    return;
+  }
   const int r0 = inv ? inv[t * k] : t * k;
   float4 acc = r0 >= 0 ? y4[(size_t)r0 * H4 + c] : z;
 #pragma unroll 8
