@@ -907,6 +907,21 @@ __device__ __forceinline__ void load_bs32z_lds(bs32z<NO> &b, const u32x4_t *bl, 
   }
 }
 
+template <int NO, int OB>
+__device__ __forceinline__ void load_bs32z_lds_v(bs32z<NO> &b, const u32x4_t *bl, const zoff &z, int step) {
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    b.lo[o] = bl[o * OB + step * 65 + z.lo];
+    b.hi[o] = bl[o * OB + step * 65 + z.hi];
+  }
+}
+
+template <int NO, int OD>
+__device__ __forceinline__ void load_bs32z_lds_d(bs32z<NO> &b, const float *dl, int dlo, int step) {
+#pragma unroll
+  for (int o = 0; o < NO; o++) b.d[o] = dl[o * OD + step * 16 + dlo];
+}
+
 // Step J of a quad (op_sel SEL = quad % 4): acc[o] += d[o] * (A . B[o]) for
 // one weight stream; the per-octet sequence is that of quad_mma32 (same bits).
 template <int SEL, int J, int NO>
@@ -928,13 +943,52 @@ __device__ __forceinline__ void step_mma32z(const wq32<1> &w, const uint32_t (&s
   for (int o = 0; o < NO; o++) asm volatile("" : "+v"(acc[o][0]));
 }
 
-// Ring of the step-B loop: weights of 3 quads (2 ahead) of one stream,
-// exponent dwords of NG groups, B of the next step (a zero-slot operand,
-// read from LDS right after the previous step's MFMAs are issued; a deeper
-// B ring does not fit 128 registers).
+// step_mma32z in two parts: the NO MFMAs of the step (results and scales
+// kept), then the scaling into acc (same operations per octet, same bits),
+// so the next step's B can be read from LDS between the two.
+template <int NO>
+struct stepres {
+  f32x16_t r[NO];
+};
+
+template <int SEL, int J, int NO>
+__device__ __forceinline__ void step_mma32z_issue(const u32x4_t &a4, const uint32_t (&sc)[1][2], const bs32z<NO> &b,
+                                                  int sb, stepres<NO> &res) {
+  const i32x8_t a = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    const u32x4_t l = b.lo[o], h = b.hi[o];
+    const i32x8_t bv = {(int)l.x, (int)l.y, (int)l.z, (int)l.w, (int)h.x, (int)h.y, (int)h.z, (int)h.w};
+    f32x16_t z;
+#pragma unroll
+    for (int e = 0; e < 16; e++) z[e] = 0.0f;
+    res.r[o] = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bv, z, 4, 0, SEL, (int)sc[0][J], 0, sb);
+  }
+}
+
+template <int NO>
+__device__ __forceinline__ void step_scale(const stepres<NO> &res, const float (&d)[NO], f32x16_t (&acc)[NO][1]) {
+#pragma unroll
+  for (int o = 0; o < NO; o++) acc[o][0] = acc[o][0] + d[o] * res.r[o];
+#pragma unroll
+  for (int o = 0; o < NO; o++) asm volatile("" : "+v"(acc[o][0]));
+}
+
+// One step's weights (step S = 2 * quad + j of the stream).
+__device__ __forceinline__ void load_w32step(u32x4_t &w, const wstream (&ws)[1], const aoff32 &ao, int S) {
+  const int q = S >> 1, j = S & 1;
+  w = __builtin_amdgcn_raw_buffer_load_b128(ws[0].rec, ao.v + j * 512, (q >> 2) * MOE_REC_BYTES + (q & 3) * 1024, 0);
+}
+
+#define MOE_DRS 4  // weight ring of the down step loop, in steps
+
+// Ring of the step-B loop: weights of MOE_DRS steps (3 ahead) of one
+// stream, exponent dwords of NG groups, B of the next step (a zero-slot
+// operand, read from LDS between the step's MFMAs and its scaling, so the
+// LDS latency overlaps them; a deeper B ring does not fit 128 registers).
 template <int NO, int NG>
 struct sring {
-  wq32<1> w[3];
+  u32x4_t w[MOE_DRS];  // weights of steps S .. S + MOE_DRS - 1 (slot S % MOE_DRS)
   uint32_t sc[NG][1][2];
   bs32z<NO> b[1];
 };
@@ -946,15 +1000,33 @@ __device__ __forceinline__ void slfixed_from(sring<NO, NG> &r, const wstream (&w
                                              f32x16_t (&acc)[NO][1]) {
   if constexpr (QL < NQW) {
     if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
-    if constexpr (QL + 2 < NQW) load_wq32<1, 0>(r.w[(QL + 2) % 3], ws, ao, QL + 2);
+    constexpr int S0 = 2 * QL, RS = MOE_DRS;
+    if constexpr (S0 + RS - 1 < 2 * NQW) load_w32step(r.w[(S0 + RS - 1) % RS], ws, ao, S0 + RS - 1);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32z<QL & 3, 0, NO>(r.w[QL % 3], r.sc[QL >> 2], r.b[0], sb, acc);
-    load_bs32z_lds<NO, OB, OD>(r.b[0], bl, dl, z, dlo, 2 * QL + 1);
+    {
+      stepres<NO> res;
+      step_mma32z_issue<QL & 3, 0, NO>(r.w[S0 % RS], r.sc[QL >> 2], r.b[0], sb, res);
+      __builtin_amdgcn_sched_barrier(0);
+      load_bs32z_lds_v<NO, OB>(r.b[0], bl, z, 2 * QL + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      step_scale<NO>(res, r.b[0].d, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_bs32z_lds_d<NO, OD>(r.b[0], dl, dlo, 2 * QL + 1);
+    }
+    if constexpr (S0 + RS < 2 * NQW) load_w32step(r.w[(S0 + RS) % RS], ws, ao, S0 + RS);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32z<QL & 3, 1, NO>(r.w[QL % 3], r.sc[QL >> 2], r.b[0], sb, acc);
-    if constexpr (QL + 1 < NQW) load_bs32z_lds<NO, OB, OD>(r.b[0], bl, dl, z, dlo, 2 * QL + 2);
+    {
+      stepres<NO> res;
+      step_mma32z_issue<QL & 3, 1, NO>(r.w[(S0 + 1) % RS], r.sc[QL >> 2], r.b[0], sb, res);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (QL + 1 < NQW) load_bs32z_lds_v<NO, OB>(r.b[0], bl, z, 2 * QL + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      step_scale<NO>(res, r.b[0].d, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (QL + 1 < NQW) load_bs32z_lds_d<NO, OD>(r.b[0], dl, dlo, 2 * QL + 2);
+    }
     slfixed_from<QL + 1, NQW, NO, NG, OB, OD>(r, ws, ao, bl, dl, z, dlo, sb, acc);
   }
 }
@@ -976,8 +1048,9 @@ __device__ __forceinline__ void dn_ol_octets(const wstream (&ws)[1], const aoff3
   sring<NO, NG> r;
   // first weights in flight during the staging
   load_sc32<1>(r.sc[0], ws, ao, 0);
-  load_wq32<1, 0>(r.w[0], ws, ao, 0);
-  if (NQ > 1) load_wq32<1, 0>(r.w[1], ws, ao, 1);
+#pragma unroll
+  for (int i = 0; i + 1 < MOE_DRS; i++)
+    if (i < 2 * NQ) load_w32step(r.w[i], ws, ao, i);
 #pragma unroll
   for (int o = 0; o < NO; o++) {
     uint32_t *ol = lds + o * OW;
@@ -1061,8 +1134,11 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 // thus crosses the vector-memory unit once per workgroup; a wave reads both
 // halves of each MFMA operand from LDS (the half without data from the zero
 // slot, so no selects) right after the previous step's MFMAs, and holds one
-// weight stream with a ring of 2 quads: 122 VGPRs, 4 waves per SIMD, which
-// beat deeper rings at 3 waves.  After the K loop gate and up meet in LDS
+// weight stream with a ring of 3 steps: 126 VGPRs, 4 waves per SIMD, which
+// beat deeper rings at 3 waves.  Each step issues its MFMAs (one result
+// register set per octet), then the next step's B reads, then the scaling
+// FMAs, so the LDS round trip overlaps the MFMAs and the FMAs instead of
+// following them.  After the K loop gate and up meet in LDS
 // for clamp + SwiGLU + Q8_0(h) as in k_gate_up_o.
 #define MOE_GCH 4                                  // quads per staged chunk
 #define MOE_GCH_STEPS (2 * MOE_GCH)                // MFMA steps per chunk
@@ -1089,11 +1165,10 @@ struct gstage_regs {
   float d;
 };
 
-// Half P of a chunk's staging (pieces m = 2P, 2P+1, or the one piece when a
-// thread has one; the scales with the last half), carried in registers from
-// its loads to its LDS stores.
+// Part P of a chunk's staging (piece m = P; the scales with the last part),
+// carried in registers from its load to its LDS store.
 struct gstage_half {
-  u32x4_t v[2];
+  u32x4_t v[1];
   float d;
 };
 
@@ -1122,10 +1197,11 @@ __device__ __forceinline__ void gstage_load(gstage_regs<NO, NU> &s, const gsrc &
   s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
 }
 
-// The staging of one chunk in halves of up to 2 pieces.
+// The staging of one chunk in NH parts of one piece each (one part live at
+// a time keeps the wave within 128 VGPRs).
 template <int NO, int NU>
 struct ghalves {
-  static constexpr int PT = gstage<NO, NU>::PT, HS = PT < 2 ? PT : 2, NH = PT / HS;
+  static constexpr int PT = gstage<NO, NU>::PT, HS = 1, NH = PT / HS;
 };
 
 template <int NO, int NU, int C, int P>
@@ -1165,6 +1241,24 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The digits (lo, hi) and the scales of one step's B, read apart.
+template <int NO>
+__device__ __forceinline__ void load_bs32_chunk_v(bs32z<NO> &b, const uint32_t *buf, const zoff &z, int ls) {
+  const u32x4_t *bl = reinterpret_cast<const u32x4_t *>(buf);
+#pragma unroll
+  for (int o = 0; o < NO; o++) {
+    b.lo[o] = bl[o * MOE_GCH_OCT_U4 + ls * 65 + z.lo];
+    b.hi[o] = bl[o * MOE_GCH_OCT_U4 + ls * 65 + z.hi];
+  }
+}
+
+template <int NO>
+__device__ __forceinline__ void load_bs32_chunk_d(bs32z<NO> &b, const uint32_t *buf, int dlo, int ls) {
+  const float *dl = reinterpret_cast<const float *>(buf) + 2 * MOE_GCH_OCT_U4 * 4;
+#pragma unroll
+  for (int o = 0; o < NO; o++) b.d[o] = dl[o * MOE_GCH_OCT_D + ls * 16 + dlo];
+}
+
 template <int NO>
 __device__ __forceinline__ void load_bs32_chunk(bs32z<NO> &b, const uint32_t *buf, const zoff &z, int dlo, int ls) {
   load_bs32z_lds<NO, MOE_GCH_OCT_U4, MOE_GCH_OCT_D>(b, reinterpret_cast<const u32x4_t *>(buf),
@@ -1174,7 +1268,7 @@ __device__ __forceinline__ void load_bs32_chunk(bs32z<NO> &b, const uint32_t *bu
 
 template <int NO, int NG>
 struct gring {
-  wq32<1> w[2];
+  u32x4_t w[3];  // weights of steps S, S+1, S+2 (slot S % 3)
   uint32_t sc[NG][1][2];
   bs32z<NO> b[1];
   gstage_half stg;
@@ -1188,21 +1282,39 @@ __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1]
   if constexpr (QL < NQ) {
     constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH;
     const uint32_t *buf = lds + (C & 1) * MOE_GCH_BUF_DW;
-    // the next chunk's staging in halves: loads at quads 0 and 2 of this
+    // the next chunk's staging in parts: loads at quads 0 and 2 of this
     // chunk, LDS stores at the ends of quads 1 and 3
     constexpr int NH = ghalves<NO, NU>::NH;
     if constexpr (C + 1 < NC && (QC & 1) == 0 && QC / 2 < NH)
       gstage_load_half<NO, NU, C + 1, QC / 2>(r.stg, src, g);
     if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
-    if constexpr (QL + 1 < NQ) load_wq32<1, 0>(r.w[(QL + 1) & 1], ws, ao, QL + 1);
+    constexpr int S0 = 2 * QL;
+    if constexpr (QL + 1 < NQ) load_w32step(r.w[(S0 + 2) % 3], ws, ao, S0 + 2);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32z<QL & 3, 0, NO>(r.w[QL & 1], r.sc[QL >> 2], r.b[0], sb, acc);
-    load_bs32_chunk<NO>(r.b[0], buf, z, dlo, 2 * QC + 1);
+    {
+      stepres<NO> res;
+      step_mma32z_issue<QL & 3, 0, NO>(r.w[S0 % 3], r.sc[QL >> 2], r.b[0], sb, res);
+      __builtin_amdgcn_sched_barrier(0);
+      load_bs32_chunk_v<NO>(r.b[0], buf, z, 2 * QC + 1);
+      __builtin_amdgcn_sched_barrier(0);
+      step_scale<NO>(res, r.b[0].d, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      load_bs32_chunk_d<NO>(r.b[0], buf, dlo, 2 * QC + 1);
+    }
+    if constexpr (QL + 1 < NQ) load_w32step(r.w[(S0 + 3) % 3], ws, ao, S0 + 3);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
-    step_mma32z<QL & 3, 1, NO>(r.w[QL & 1], r.sc[QL >> 2], r.b[0], sb, acc);
-    if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk<NO>(r.b[0], buf, z, dlo, 2 * QC + 2);
+    {
+      stepres<NO> res;
+      step_mma32z_issue<QL & 3, 1, NO>(r.w[(S0 + 1) % 3], r.sc[QL >> 2], r.b[0], sb, res);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk_v<NO>(r.b[0], buf, z, 2 * QC + 2);
+      __builtin_amdgcn_sched_barrier(0);
+      step_scale<NO>(res, r.b[0].d, acc);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk_d<NO>(r.b[0], buf, dlo, 2 * QC + 2);
+    }
     if constexpr (C + 1 < NC && (QC & 1) == 1 && QC / 2 < NH)
       gstage_store_half<NO, NU, QC / 2>(r.stg, lds + ((C + 1) & 1) * MOE_GCH_BUF_DW, g, tid);
     if constexpr (QC + 1 == MOE_GCH && C + 1 < NC) {
@@ -1228,7 +1340,8 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
   gring<NO, NG> r;
   // first weights in flight during the first staging
   load_sc32<1>(r.sc[0], ws, ao, 0);
-  load_wq32<1, 0>(r.w[0], ws, ao, 0);
+  load_w32step(r.w[0], ws, ao, 0);
+  load_w32step(r.w[1], ws, ao, 1);
   {
     gstage_regs<NO, NU> s0;  // chunk 0 in one go: nothing else is in the ring yet
     gstage_load<NO, NU, 0>(s0, src, g);
