@@ -17,6 +17,7 @@
 #define MOE_GROUP_MAX_E 1024
 #define MOE_GROUP_MAX_PAIRS 65535  // grouped rows are kept in 16 bits in k_group
 #define MOE_GROUP_QBLOCKS 512  // x blocks quantized per extra workgroup of k_group
+#define MOE_GROUP_IT 8         // 64-pair steps per wave whose ids k_group keeps in registers
 
 // Item capacity of a call with T tokens, top-k, E experts and items of at
 // most BT rows: ceil(c_e / BT) per expert sums to at most P/BT + min(P, E),
@@ -81,15 +82,42 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
   __shared__ int32_t wsum[16], wsumi[16], wsumi2[16], tot[2];
   const int PW = ((P + 15) / 16 + 63) & ~63;    // pairs per wave, whole steps of 64
   const int p_lo = wave * PW, p_hi = p_lo + PW < P ? p_lo + PW : P;
+  // up to MOE_GROUP_IT steps of 64 pairs per wave (P <= 16 * 64 * MOE_GROUP_IT):
+  // the wave's ids are loaded at once and kept, with each lane's rank among
+  // the lanes of its step with the same id, for pass 2
+  const bool cached = p_hi - p_lo <= 64 * MOE_GROUP_IT;
+  int ev[MOE_GROUP_IT];
+  uint32_t rl[MOE_GROUP_IT];  // rank | (last lane of its id in the step) << 16
+  if (cached) {
+#pragma unroll
+    for (int it = 0; it < MOE_GROUP_IT; it++) {
+      const int p = p_lo + 64 * it + lane;
+      ev[it] = p < p_hi ? ids[p] : -1;
+    }
+  }
   for (int i = tid; i < 16 * MOE_GROUP_MAX_E; i += 1024) (&wc[0][0])[i] = 0;
   __syncthreads();
-  for (int pb = p_lo; pb < p_hi; pb += 64) {
-    const int p = pb + lane;
-    const int e = p < p_hi ? ids[p] : -1;
-    const bool ok = e >= 0 && e < E;  // out-of-range ids are dropped (the host validates the ids it owns)
-    const uint64_t m = same_id_lanes(e, ok);
-    const uint64_t below = (1ull << lane) - 1ull, upto = (2ull << lane) - 1ull;
-    if (ok && !(m & ~upto)) wc[wave][e] += (uint16_t)__popcll(m & below) + 1;  // last lane of its expert
+  const uint64_t below = (1ull << lane) - 1ull, upto = (2ull << lane) - 1ull;
+  if (cached) {
+#pragma unroll
+    for (int it = 0; it < MOE_GROUP_IT; it++) {
+      if (p_lo + 64 * it >= p_hi) break;  // uniform over the wave
+      const int e = ev[it];
+      const bool ok = e >= 0 && e < E;  // out-of-range ids are dropped (the host validates the ids it owns)
+      const uint64_t m = same_id_lanes(e, ok);
+      const int rank = __popcll(m & below);
+      const bool last = !(m & ~upto);
+      rl[it] = (uint32_t)rank | (last ? 1u << 16 : 0u);
+      if (ok && last) wc[wave][e] += (uint16_t)rank + 1;  // last lane of its expert
+    }
+  } else {
+    for (int pb = p_lo; pb < p_hi; pb += 64) {
+      const int p = pb + lane;
+      const int e = p < p_hi ? ids[p] : -1;
+      const bool ok = e >= 0 && e < E;
+      const uint64_t m = same_id_lanes(e, ok);
+      if (ok && !(m & ~upto)) wc[wave][e] += (uint16_t)__popcll(m & below) + 1;
+    }
   }
   __syncthreads();
   // histogram and exclusive scans over experts of the counts and the item counts
@@ -163,13 +191,10 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     }
     if (tid == 0) items2[0] = tot[1] + ns;
   }
-  for (int pb = p_lo; pb < p_hi; pb += 64) {
-    const int p = pb + lane;
-    const int e = p < p_hi ? ids[p] : -1;
+  // pass 2: row of a pair = wc[w][e] + rank (the lanes of one id read wc
+  // before the last of them advances it)
+  auto place = [&](int p, int e, int rank, bool last) {
     const bool ok = e >= 0 && e < E;
-    const uint64_t m = same_id_lanes(e, ok);
-    const uint64_t below = (1ull << lane) - 1ull, upto = (2ull << lane) - 1ull;
-    const int rank = __popcll(m & below);
     if (ok) {
       const int pos = wc[wave][e] + rank;
       perm[pos] = p;
@@ -177,7 +202,21 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     } else if (p < p_hi && inv) {
       inv[p] = -1;  // dropped pair: no grouped row
     }
-    if (ok && !(m & ~upto)) wc[wave][e] += (uint16_t)(rank + 1);
+    if (ok && last) wc[wave][e] += (uint16_t)(rank + 1);
+  };
+  if (cached) {
+#pragma unroll
+    for (int it = 0; it < MOE_GROUP_IT; it++) {
+      if (p_lo + 64 * it >= p_hi) break;
+      place(p_lo + 64 * it + lane, ev[it], (int)(rl[it] & 0xffffu), (rl[it] >> 16) != 0);
+    }
+  } else {
+    for (int pb = p_lo; pb < p_hi; pb += 64) {
+      const int p = pb + lane;
+      const int e = p < p_hi ? ids[p] : -1;
+      const uint64_t m = same_id_lanes(e, e >= 0 && e < E);
+      place(p, e, __popcll(m & below), !(m & ~upto));
+    }
   }
 }
 

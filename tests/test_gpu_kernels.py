@@ -122,8 +122,11 @@ def test_route_matches_oracle(blk, torch_dev, oracle, mode, E, k, T, bias):
     np.testing.assert_allclose(wts.cpu().numpy(), ow, rtol=2e-6, atol=1e-7)
 
 
+# P = 8800 (T = 1100): more than 8 steps of 64 pairs per wave, past the ids
+# k_group keeps in registers
 @pytest.mark.parametrize("T,k,E,zipf", [(1, 8, 256, False), (4, 8, 256, True), (64, 8, 256, True),
-                                        (512, 8, 256, True), (512, 8, 256, False), (3, 4, 32, False)])
+                                        (512, 8, 256, True), (512, 8, 256, False), (3, 4, 32, False),
+                                        (1100, 8, 256, True), (1100, 8, 256, False)])
 def test_group_bit_exact(blk, torch_dev, oracle, T, k, E, zipf):
     torch, dev = torch_dev
     shape = wl.LayerShape(hidden=64, ffn=64, n_expert=E, n_used=k, has_shared=False, route_mode=1)
@@ -142,7 +145,7 @@ def test_group_bit_exact(blk, torch_dev, oracle, T, k, E, zipf):
         np.testing.assert_array_equal(t.cpu().numpy(), g[name], err_msg=name)
 
 
-@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32)])
+@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32), (1100, 8, 256)])
 def test_group_drops_out_of_range_ids(blk, torch_dev, T, k, E):
     """Out-of-range ids get no grouped row (inv = -1); the valid pairs keep
     ascending pair order within each expert (checked against a stable sort)."""
