@@ -1128,117 +1128,73 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 // all of K against the item's one or two octets.  The workgroup copies
 // B (the octets' x rows) into LDS in chunks of MOE_GCH quads, already in
 // MFMA lane order (the layout of stage_octet_lds, per chunk, each step's 64
-// lanes followed by a 16-byte zero slot), double buffered: the global loads
-// of chunk c+1 are issued in two halves during chunk c and written to the
-// other buffer one quad later, then one barrier at its end.  Every B byte
-// thus crosses the vector-memory unit once per workgroup; a wave reads both
-// halves of each MFMA operand from LDS (the half without data from the zero
-// slot, so no selects) right after the previous step's MFMAs, and holds one
-// weight stream with a ring of 3 steps: 126 VGPRs, 4 waves per SIMD, which
-// beat deeper rings at 3 waves.  Each step issues its MFMAs (one result
-// register set per octet), then the next step's B reads, then the scaling
-// FMAs, so the LDS round trip overlaps the MFMAs and the FMAs instead of
-// following them.  After the K loop gate and up meet in LDS
-// for clamp + SwiGLU + Q8_0(h) as in k_gate_up_o.
+// lanes followed by a 16-byte zero slot), double buffered: chunk c+1 goes
+// out at chunk c's first quad as direct global-to-LDS loads and is waited
+// for only at the chunk's end barrier.  Every B byte thus crosses the
+// vector-memory unit once per workgroup and never occupies a VGPR; a wave
+// reads both halves of each MFMA operand from LDS (the half without data
+// from the zero slot, so no selects) and holds one weight stream with a
+// ring of MOE_GU_RS steps: 128 VGPRs, 4 waves per SIMD, which beat deeper
+// rings at 3 waves.  Each step issues its MFMAs (one result register set
+// per octet), then the next step's B reads, then the scaling FMAs, so the
+// LDS round trip overlaps the MFMAs and the FMAs instead of following them.
+// After the K loop gate and up meet in LDS for clamp + SwiGLU + Q8_0(h) as
+// in k_gate_up_o.
 #define MOE_GCH 4                                  // quads per staged chunk
 #define MOE_GCH_STEPS (2 * MOE_GCH)                // MFMA steps per chunk
 #define MOE_GCH_OCT_U4 (MOE_GCH_STEPS * 65)        // 16-byte units per octet per chunk (digits, zero slots)
 #define MOE_GCH_OCT_D (MOE_GCH_STEPS * 16)         // scales per octet per chunk
 #define MOE_GCH_BUF_DW (2 * MOE_GCH_OCT_U4 * 4 + 2 * MOE_GCH_OCT_D)  // dwords per chunk buffer (two octets)
 
-// This thread's part of the staging, for a workgroup of 128*NU threads:
-// PT = 4*NO/NU 16-byte digit pieces of tokens t = tid/64 + 2*NU*m (m < PT)
-// at block b = (tid%64)/4, piece sub = tid%4 of each chunk, and (tid <
-// 128*NO) the scale of token tid/16, block tid%16.
-template <int NO, int NU>
-struct gstage {
-  static constexpr int PT = 4 * NO / NU;  // pieces per thread and chunk
-  uint32_t xo[PT];                        // byte offset in the digit rows at chunk 0 (MOE_OOB: absent token)
-  int lu4[PT];                            // 16-byte unit in the chunk buffer
-  uint32_t dof;                           // byte offset in the scale rows at chunk 0
-  int ld;                                 // float index in the chunk buffer
-};
-
-template <int NO, int NU>
-struct gstage_regs {
-  u32x4_t v[4 * NO / NU];
-  float d;
-};
-
-// Part P of a chunk's staging (piece m = P; the scales with the last part),
-// carried in registers from its load to its LDS store.
-struct gstage_half {
-  u32x4_t v[1];
-  float d;
-};
-
-template <int NO, int NU>
-__device__ __forceinline__ gstage<NO, NU> make_gstage(int tid, const int (&xr)[4 * NO / NU], int xr_d, int KB) {
-  gstage<NO, NU> g;
-  const int w = tid & 63, b = w >> 2, sub = w & 3;
-#pragma unroll
-  for (int m = 0; m < gstage<NO, NU>::PT; m++) {
-    const int t = (tid >> 6) + 2 * NU * m, o = t >> 3, tt = t & 7;
-    g.xo[m] = xr[m] >= 0 ? (uint32_t)((xr[m] * KB + b) * (MOE_XSW * 4) + sub * 16) : MOE_OOB;
-    g.lu4[m] = o * MOE_GCH_OCT_U4 + (b >> 1) * 65 + 32 * (sub & 1) + 4 * tt + 2 * (sub >> 1) + (b & 1);
-  }
-  const int td = tid >> 4, bd = tid & 15;
-  g.dof = xr_d >= 0 ? (uint32_t)((xr_d * KB + bd) * 4) : MOE_OOB;
-  g.ld = 2 * MOE_GCH_OCT_U4 * 4 + (td >> 3) * MOE_GCH_OCT_D + (bd >> 1) * 16 + (td & 7) * 2 + (bd & 1);
-  return g;
-}
-
-// Global loads of chunk C (blocks 16*C .. 16*C + 15 of every row).
-template <int NO, int NU, int C>
-__device__ __forceinline__ void gstage_load(gstage_regs<NO, NU> &s, const gsrc &src, const gstage<NO, NU> &g) {
-#pragma unroll
-  for (int m = 0; m < gstage<NO, NU>::PT; m++)
-    s.v[m] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[m], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
-  s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
-}
-
-// The staging of one chunk in NH parts of one piece each (one part live at
-// a time keeps the wave within 128 VGPRs).
-template <int NO, int NU>
-struct ghalves {
-  static constexpr int PT = gstage<NO, NU>::PT, HS = 1, NH = PT / HS;
-};
-
-template <int NO, int NU, int C, int P>
-__device__ __forceinline__ void gstage_load_half(gstage_half &s, const gsrc &src, const gstage<NO, NU> &g) {
-  constexpr int HS = ghalves<NO, NU>::HS, NH = ghalves<NO, NU>::NH;
-#pragma unroll
-  for (int i = 0; i < HS; i++)
-    s.v[i] = __builtin_amdgcn_raw_buffer_load_b128(src.x, g.xo[HS * P + i], C * 4 * MOE_GCH * MOE_XSW * 4, 0);
-  if constexpr (P == NH - 1)
-    s.d = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(src.d, g.dof, C * 4 * MOE_GCH * 4, 0));
-}
-
-template <int NO, int NU, int P>
-__device__ __forceinline__ void gstage_store_half(const gstage_half &s, uint32_t *buf, const gstage<NO, NU> &g,
-                                                  int tid) {
-  constexpr int HS = ghalves<NO, NU>::HS, NH = ghalves<NO, NU>::NH;
-  u32x4_t *bu = reinterpret_cast<u32x4_t *>(buf);
-#pragma unroll
-  for (int i = 0; i < HS; i++) bu[g.lu4[HS * P + i]] = s.v[i];
-  if constexpr (P == NH - 1)
-    if (tid < 128 * NO) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // the scales of the present octets
-}
-
-template <int NO, int NU>
-__device__ __forceinline__ void gstage_store(const gstage_regs<NO, NU> &s, uint32_t *buf, const gstage<NO, NU> &g,
-                                             int tid) {
-  u32x4_t *bu = reinterpret_cast<u32x4_t *>(buf);
-#pragma unroll
-  for (int m = 0; m < gstage<NO, NU>::PT; m++) bu[g.lu4[m]] = s.v[m];
-  if (tid < 128 * NO) reinterpret_cast<float *>(buf)[g.ld] = s.d;  // the scales of the present octets
-}
-
 // LDS writes of this wave done, then the workgroup barrier.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
+// in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+__host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+
+// The staging of a chunk by direct global-to-LDS loads (buffer_load ... lds):
+// a wave's loads write 64 consecutive 16-byte units (one octet's step, lane
+// u = unit u) or 64 consecutive scales, so the data never passes through
+// VGPRs.  Unit u of a step holds token (u>>2)&7, block 2*step + (u&1) of the
+// chunk and 16-byte piece (u>>5) | ((u>>1)&1)<<1 of that block; scale f of
+// an octet's 128 holds token (f>>1)&7 of block 2*(f>>4) + (f&1).  Of the
+// 8*NO (octet, step) loads of a chunk wave w issues w*NO .. w*NO+NO-1 (all
+// of one octet), and waves 0 .. 2*NO-1 one half of an octet's scales each.
+// The loads of chunk c+1 go out at chunk c's first quad; the wave waits for
+// them (vmcnt) only right before the chunk's end barrier.
+struct gdma {
+  uint32_t xo;  // this lane's digit bytes at chunk 0 (MOE_OOB: absent token)
+  uint32_t so;  // this lane's scale at chunk 0 (MOE_OOB: absent, or no scale load for this wave)
+};
+
+template <int NO>
+__device__ __forceinline__ gdma make_gdma(int lane, int wave, int xr_dig, int xr_sc, int KB) {
+  gdma g;
+  const int sub = (lane >> 5) | (((lane >> 1) & 1) << 1);
+  g.xo = xr_dig >= 0 ? (uint32_t)((xr_dig * KB + (lane & 1)) * (MOE_XSW * 4) + sub * 16) : MOE_OOB;
+  g.so = (wave < 2 * NO && xr_sc >= 0) ? (uint32_t)((xr_sc * KB + 2 * (lane >> 4) + (lane & 1)) * 4) : MOE_OOB;
+  return g;
+}
+
+template <int NO, int NX, int C>
+__device__ __forceinline__ void gdma_issue(const gdma &g, const gsrc &src, uint32_t *buf, int wave) {
+  typedef __attribute__((address_space(3))) void *lds_t;
+#pragma unroll
+  for (int j = 0; j < NO; j++) {
+    const int i = wave * NO + j, o = i >> 3, st = i & 7;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_t)(buf + (o * MOE_GCH_OCT_U4 + st * 65) * 4), 16, g.xo,
+                                             (16 * C + 2 * st) * (MOE_XSW * 4), 0, 0);
+  }
+  if (wave < 2 * NO) {
+    const int o = wave >> 1, hh = wave & 1;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.d, (lds_t)(buf + NX * MOE_GCH_OCT_U4 * 4 + o * MOE_GCH_OCT_D + hh * 64),
+                                             4, g.so, (16 * C + 8 * hh) * 4, 0, 0);
+  }
 }
 
 // The digits (lo, hi) and the scales of one step's B, read apart.
@@ -1266,35 +1222,52 @@ __device__ __forceinline__ void load_bs32_chunk(bs32z<NO> &b, const uint32_t *bu
                                                     dlo, ls);
 }
 
+#define MOE_GU_RS 4  // weight ring of the gate/up step loop, in steps (3 ahead)
+
 template <int NO, int NG>
 struct gring {
-  u32x4_t w[3];  // weights of steps S, S+1, S+2 (slot S % 3)
+  u32x4_t w[MOE_GU_RS];  // weights of steps S .. S + MOE_GU_RS - 1 (slot S % MOE_GU_RS)
   uint32_t sc[NG][1][2];
   bs32z<NO> b[1];
-  gstage_half stg;
 };
 
+// VMEM loads a wave issues after its chunk-C staging loads, up to the end of
+// the chunk (the exponent dwords of the next group, two weight steps a quad).
+template <int C, int NQ, int NG>
+__host__ __device__ constexpr int gdma_after() {
+  int n = 0;
+  if (C + 1 < NG) n += 2;
+  for (int qc = 0; qc < MOE_GCH; qc++) {
+    const int S0 = 2 * (MOE_GCH * C + qc);
+    if (S0 + MOE_GU_RS - 1 < 2 * NQ) n++;
+    if (S0 + MOE_GU_RS < 2 * NQ) n++;
+  }
+  return n;
+}
+
 // Quads QL .. NQ-1 of the chunked K loop.
-template <int QL, int NQ, int NO, int NU, int NG>
-__device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
-                                        const gstage<NO, NU> &g, uint32_t *lds, int tid, const zoff &z, int dlo,
-                                        int sb, f32x16_t (&acc)[NO][1]) {
+template <int QL, int NQ, int NO, int NG>
+__device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1], const aoff32 &ao,
+                                        const gsrc &src, const gdma &g, uint32_t *lds, int wave, const zoff &z,
+                                        int dlo, int sb, f32x16_t (&acc)[NO][1]) {
   if constexpr (QL < NQ) {
-    constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH;
+    constexpr int C = QL / MOE_GCH, QC = QL % MOE_GCH, NC = NQ / MOE_GCH, RS = MOE_GU_RS;
     const uint32_t *buf = lds + (C & 1) * MOE_GCH_BUF_DW;
-    // the next chunk's staging in parts: loads at quads 0 and 2 of this
-    // chunk, LDS stores at the ends of quads 1 and 3
-    constexpr int NH = ghalves<NO, NU>::NH;
-    if constexpr (C + 1 < NC && (QC & 1) == 0 && QC / 2 < NH)
-      gstage_load_half<NO, NU, C + 1, QC / 2>(r.stg, src, g);
+    if constexpr (C + 1 < NC && QC == 0) {  // the next chunk's staging, straight into the other buffer
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      gdma_issue<NO, 2, C + 1>(g, src, lds + ((C + 1) & 1) * MOE_GCH_BUF_DW, wave);
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+    }
     if constexpr ((QL & 3) == 0 && (QL >> 2) + 1 < NG) load_sc32<1>(r.sc[(QL >> 2) + 1], ws, ao, (QL >> 2) + 1);
     constexpr int S0 = 2 * QL;
-    if constexpr (QL + 1 < NQ) load_w32step(r.w[(S0 + 2) % 3], ws, ao, S0 + 2);
+    if constexpr (S0 + RS - 1 < 2 * NQ) load_w32step(r.w[(S0 + RS - 1) % RS], ws, ao, S0 + RS - 1);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     {
       stepres<NO> res;
-      step_mma32z_issue<QL & 3, 0, NO>(r.w[S0 % 3], r.sc[QL >> 2], r.b[0], sb, res);
+      step_mma32z_issue<QL & 3, 0, NO>(r.w[S0 % RS], r.sc[QL >> 2], r.b[0], sb, res);
       __builtin_amdgcn_sched_barrier(0);
       load_bs32_chunk_v<NO>(r.b[0], buf, z, 2 * QC + 1);
       __builtin_amdgcn_sched_barrier(0);
@@ -1302,12 +1275,12 @@ __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1]
       __builtin_amdgcn_sched_barrier(0);
       load_bs32_chunk_d<NO>(r.b[0], buf, dlo, 2 * QC + 1);
     }
-    if constexpr (QL + 1 < NQ) load_w32step(r.w[(S0 + 3) % 3], ws, ao, S0 + 3);
+    if constexpr (S0 + RS < 2 * NQ) load_w32step(r.w[(S0 + RS) % RS], ws, ao, S0 + RS);
     asm volatile("" ::: "memory");
     __builtin_amdgcn_sched_barrier(0);
     {
       stepres<NO> res;
-      step_mma32z_issue<QL & 3, 1, NO>(r.w[(S0 + 1) % 3], r.sc[QL >> 2], r.b[0], sb, res);
+      step_mma32z_issue<QL & 3, 1, NO>(r.w[(S0 + 1) % RS], r.sc[QL >> 2], r.b[0], sb, res);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk_v<NO>(r.b[0], buf, z, 2 * QC + 2);
       __builtin_amdgcn_sched_barrier(0);
@@ -1315,43 +1288,48 @@ __device__ __forceinline__ void gl_from(gring<NO, NG> &r, const wstream (&ws)[1]
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (QC + 1 < MOE_GCH) load_bs32_chunk_d<NO>(r.b[0], buf, dlo, 2 * QC + 2);
     }
-    if constexpr (C + 1 < NC && (QC & 1) == 1 && QC / 2 < NH)
-      gstage_store_half<NO, NU, QC / 2>(r.stg, lds + ((C + 1) & 1) * MOE_GCH_BUF_DW, g, tid);
     if constexpr (QC + 1 == MOE_GCH && C + 1 < NC) {
+      // the next chunk has landed in LDS (this wave's loads, then everyone's)
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(vmcnt_imm(gdma_after<C, NQ, NG>()));
       uint32_t *nb = lds + ((C + 1) & 1) * MOE_GCH_BUF_DW;
       lds_barrier();
       load_bs32_chunk<NO>(r.b[0], nb, z, dlo, 0);
     }
-    gl_from<QL + 1, NQ, NO, NU, NG>(r, ws, ao, src, g, lds, tid, z, dlo, sb, acc);
+    gl_from<QL + 1, NQ, NO, NG>(r, ws, ao, src, g, lds, wave, z, dlo, sb, acc);
   }
 }
 
-// The K loop of one wave (of 2*NU) against NO octets; leaves this wave's
-// sums (the 4 columns of a token added) in red[w%NU][w/NU][token][row].
-template <int NQ, int NO, int NU>
+// The K loop of one wave (of 8: NU = 4) against NO octets; xrow(i) = the
+// staged x row of the item's token i (< 0: absent).  Leaves this wave's sums
+// (the 4 columns of a token added) in red[w%NU][w/NU][token][row].
+template <int NQ, int NO, int NU, class XR>
 __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
-                                             const int (&xr)[8 / NU], int xr_d, int KB, uint32_t *lds, int tid,
-                                             int wave, int lane) {
-  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, PT = gstage<NO, NU>::PT;
-  int xrm[PT];
-#pragma unroll
-  for (int m = 0; m < PT; m++) xrm[m] = xr[m];
-  const gstage<NO, NU> g = make_gstage<NO, NU>(tid, xrm, xr_d, KB);
+                                             const XR &xrow, int KB, uint32_t *lds, int tid, int wave, int lane) {
+  static_assert(NU == 4, "the staging loads are laid out for 8 waves");
+  constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, RS = MOE_GU_RS;
+  const int xr_dig = xrow(8 * ((wave * NO) >> 3) + ((lane >> 2) & 7));
+  const int xr_sc = wave < 2 * NO ? xrow(8 * (wave >> 1) + ((lane >> 1) & 7)) : -1;
+  const gdma g = make_gdma<NO>(lane, wave, xr_dig, xr_sc, KB);
   gring<NO, NG> r;
-  // first weights in flight during the first staging
+  // chunk 0 straight into LDS, then the first weights
+  gdma_issue<NO, 2, 0>(g, src, lds, wave);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   load_sc32<1>(r.sc[0], ws, ao, 0);
-  load_w32step(r.w[0], ws, ao, 0);
-  load_w32step(r.w[1], ws, ao, 1);
-  {
-    gstage_regs<NO, NU> s0;  // chunk 0 in one go: nothing else is in the ring yet
-    gstage_load<NO, NU, 0>(s0, src, g);
-    gstage_store<NO, NU>(s0, lds, g, tid);
-  }
+#pragma unroll
+  for (int i = 0; i + 1 < RS; i++)
+    if (i < 2 * NQ) load_w32step(r.w[i], ws, ao, i);
   if (tid < 2 * 2 * MOE_GCH_STEPS) {  // the zero slots of both chunk buffers, never written by the staging
     const int bf = tid / (2 * MOE_GCH_STEPS), o = (tid / MOE_GCH_STEPS) & 1, st = tid % MOE_GCH_STEPS;
     reinterpret_cast<u32x4_t *>(lds + bf * MOE_GCH_BUF_DW)[o * MOE_GCH_OCT_U4 + st * 65 + 64] =
         u32x4_t{0u, 0u, 0u, 0u};
   }
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  // the chunk-0 loads have landed (2 exponent dwords and RS-1 weight steps went out after them)
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 + (RS - 1 < 2 * NQ ? RS - 1 : 2 * NQ)));
   lds_barrier();
   const int n = lane & 31, gb = lane >> 5, t = n >> 2;
   const int dlo = t * 2 + (n & 1);
@@ -1362,7 +1340,7 @@ __device__ __forceinline__ void gu_ol_octets(const wstream (&ws)[1], const aoff3
     for (int e = 0; e < 16; e++) acc[o][0][e] = 0.0f;
   const zoff z = make_zoff(lane);
   load_bs32_chunk<NO>(r.b[0], lds, z, dlo, 0);
-  gl_from<0, NQ, NO, NU, NG>(r, ws, ao, src, g, lds, tid, z, dlo, lane_bscale32(lane), acc);
+  gl_from<0, NQ, NO, NG>(r, ws, ao, src, g, lds, wave, z, dlo, lane_bscale32(lane), acc);
   lds_barrier();  // every wave is done with the chunk buffers, which now hold the sums
   float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
@@ -1400,12 +1378,8 @@ void k_gate_up_ol(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const aoff32 ao = make_aoff32(lane, NQ4);
   const gsrc src = make_gsrc(xq, xd, T, KB);
   auto xrow = [&](int i) { return i < nt ? (shared ? row0 + i - P : perm[row0 + i] / k) : -1; };
-  int xr[8 / NU];
-#pragma unroll
-  for (int m = 0; m < 8 / NU; m++) xr[m] = xrow((tid >> 6) + 2 * NU * m);
-  const int xr_d = tid < 256 ? xrow(tid >> 4) : -1;
-  if (nt > 8) gu_ol_octets<NQ, 2, NU>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);  // uniform branch
-  else gu_ol_octets<NQ, 1, NU>(ws, ao, src, xr, xr_d, KB, lds, tid, wave, lane);
+  if (nt > 8) gu_ol_octets<NQ, 2, NU>(ws, ao, src, xrow, KB, lds, tid, wave, lane);  // uniform branch
+  else gu_ol_octets<NQ, 1, NU>(ws, ao, src, xrow, KB, lds, tid, wave, lane);
   __syncthreads();
   const float *red = reinterpret_cast<const float *>(lds);
   // (unit, token) c = 4*NU*round + 2*wave + half-wave: unit c / 16, token c % 16
