@@ -105,6 +105,84 @@ __device__ __forceinline__ void stage_quant(const float *__restrict__ x, int nb,
   }
 }
 
+// stage_quant in two parts, for callers with nb <= nthr/2 (one block half
+// per thread): the x loads go out first, ahead of the loads the caller
+// issues next (a weight ring's first quads), and the code follows; the
+// arithmetic is stage_quant's (same bits).
+struct xq_half {
+  float4 a0, a1, c0, c1;
+};
+
+__device__ __forceinline__ void stage_quant_issue(const float *__restrict__ x, int nb, int tid, xq_half &v) {
+  const int b = tid >> 1 < nb ? tid >> 1 : nb - 1, h = tid & 1;  // every lane loads (a valid block)
+  const float4 *xb = reinterpret_cast<const float4 *>(x + (size_t)b * MOE_QK + 8 * h);
+  v.a0 = xb[0];
+  v.a1 = xb[1];
+  v.c0 = xb[4];
+  v.c1 = xb[5];
+}
+
+__device__ __forceinline__ void stage_quant_finish(const xq_half &v, int nb, uint32_t *xs, float *dy, int tid) {
+  const int b = tid >> 1, h = tid & 1;
+  if (b < nb) {
+    const float lo[8] = {v.a0.x, v.a0.y, v.a0.z, v.a0.w, v.a1.x, v.a1.y, v.a1.z, v.a1.w};
+    const float hi[8] = {v.c0.x, v.c0.y, v.c0.z, v.c0.w, v.c1.x, v.c1.y, v.c1.z, v.c1.w};
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; i++) amax = fmaxf(amax, fmaxf(fabsf(lo[i]), fabsf(hi[i])));
+    amax = fmaxf(amax, dpp_f<0xB1>(amax));  // partner lane (lane ^ 1) holds the other half
+    uint32_t wh[4], wl[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float q0 = q8_code(lo[2 * i], amax), q1 = q8_code(hi[2 * i], amax);
+      const float q2 = q8_code(lo[2 * i + 1], amax), q3 = q8_code(hi[2 * i + 1], amax);
+      wh[i] = pack_e4m3x4(q_hi(q0), q_hi(q1), q_hi(q2), q_hi(q3));
+      wl[i] = pack_e4m3x4(q_lo(q0), q_lo(q1), q_lo(q2), q_lo(q3));
+    }
+    uint4 *dst = reinterpret_cast<uint4 *>(xs + (size_t)b * MOE_XSW);
+    dst[h] = make_uint4(wh[0], wh[1], wh[2], wh[3]);
+    dst[2 + h] = make_uint4(wl[0], wl[1], wl[2], wl[3]);
+    if (!h) dy[b] = (float)q8_scale_f16(amax);
+  }
+}
+
+// stage_copy<false> in two parts, for nb <= 16 * MOE_COPY_MAX blocks (at most
+// MOE_COPY_MAX 16-byte pieces and two scales per lane): loads first, LDS
+// stores after the caller's next loads are issued.
+#define MOE_COPY_MAX 8
+struct hcopy {
+  u32x4_t v[MOE_COPY_MAX];  // a clang vector type: an array of HIP's uint4 is not kept in registers
+  float d[2];
+};
+
+__device__ __forceinline__ void stage_copy_issue(const uint32_t *__restrict__ src, const float *__restrict__ sd, int nb,
+                                                 int lane, hcopy &c) {
+  // every lane loads (a valid piece); only the stores are guarded
+#pragma unroll
+  for (int j = 0; j < MOE_COPY_MAX; j++) {
+    const int i = lane + 64 * j;
+    c.v[j] = reinterpret_cast<const u32x4_t *>(src)[i < nb * 4 ? i : nb * 4 - 1];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int i = lane + 64 * j;
+    c.d[j] = sd[i < nb ? i : nb - 1];
+  }
+}
+
+__device__ __forceinline__ void stage_copy_finish(const hcopy &c, int nb, uint32_t *xs, float *dy, int lane) {
+#pragma unroll
+  for (int j = 0; j < MOE_COPY_MAX; j++) {
+    const int i = lane + 64 * j;
+    if (i < nb * 4) reinterpret_cast<u32x4_t *>(xs)[i] = c.v[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int i = lane + 64 * j;
+    if (i < nb) dy[i] = c.d[j];
+  }
+}
+
 // Copy nb staged blocks from global memory into LDS.  COHERENT: the source
 // was written by another workgroup of the same launch, so the loads are
 // agent-scope (they bypass the XCD's L2); otherwise plain loads.
@@ -709,10 +787,19 @@ __global__ __launch_bounds__(64 * MOE_BAL_WAVES) void k_gate_up_bal2(
   const wstream ws[1] = {make_wstream(mi ? w_u : w_g, (size_t)e * tiles + 2 * u + ti, NQ4)};
   kring<1, MOE_BAL_RING> ring;
   kring<1, MOE_BAL2_RING> ring8;
+  // x's loads first, then the weight rings' first quads, then x's code
+  const bool x1 = 2 * KB <= 64 * MOE_BAL_WAVES;
+  xq_half xv;
+  if (x1) stage_quant_issue(x, KB, threadIdx.x, xv);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   if (local) kloop_prime<1, MOE_BAL_RING>(ring, ws, 0, NQ, lane);
   else kloop_prime<1, MOE_BAL2_RING>(ring8, ws, 0, NQ, lane);
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
   if (threadIdx.x < 4) xs[threadIdx.x] = 0u;
-  stage_quant(x, KB, xs + 4, dy, threadIdx.x, 64 * MOE_BAL_WAVES);
+  if (x1) stage_quant_finish(xv, KB, xs + 4, dy, threadIdx.x);
+  else stage_quant(x, KB, xs + 4, dy, threadIdx.x, 64 * MOE_BAL_WAVES);
   __syncthreads();
   const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
   f32x4_t acc[1][1];
@@ -795,12 +882,24 @@ __global__ __launch_bounds__(1024) void k_down_dec(
   e = valid ? e : 0;
   const wstream ws[1] = {make_wstream(w_d, (size_t)e * tiles + tile, NQ4)};
   kring<1, 4> ring;
-  kloop_prime<1, 4>(ring, ws, 0, NQ, lane);
   uint32_t *xs = lds + (size_t)s * wave_words;
   float *dy = reinterpret_cast<float *>(xs + 4 + (size_t)nb * MOE_XSW);
   float *ys = reinterpret_cast<float *>(lds + (size_t)S * wave_words);  // [S][16]
   if (lane < 4) xs[lane] = 0u;
-  stage_copy<false>(hs + (size_t)s * U * MOE_XSW, hd + (size_t)s * U, nb, xs + 4, dy, lane);
+  if (nb <= 16 * MOE_COPY_MAX) {  // uniform: each path straight-line (a copy held across a branch goes to scratch)
+    // the slot's h loads first, then the ring's first quads, then h into LDS
+    hcopy hv;
+    stage_copy_issue(hs + (size_t)s * U * MOE_XSW, hd + (size_t)s * U, nb, lane, hv);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    kloop_prime<1, 4>(ring, ws, 0, NQ, lane);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    stage_copy_finish(hv, nb, xs + 4, dy, lane);
+  } else {
+    kloop_prime<1, 4>(ring, ws, 0, NQ, lane);
+    stage_copy<false>(hs + (size_t)s * U * MOE_XSW, hd + (size_t)s * U, nb, xs + 4, dy, lane);
+  }
   __syncthreads();
   const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
   f32x4_t acc[1][1];
