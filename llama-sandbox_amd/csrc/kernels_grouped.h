@@ -35,6 +35,17 @@ __device__ __forceinline__ int4 item_of(const int32_t *__restrict__ items, int i
   return reinterpret_cast<const int4 *>(items)[1 + i];
 }
 
+// LDS writes of this wave done, then the workgroup barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
+// in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
+__host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
+
 // Buffer resources over the staged rows (digits) and their block scales.
 struct gsrc {
   __amdgpu_buffer_rsrc_t x, d;
@@ -1033,12 +1044,47 @@ __device__ __forceinline__ void slfixed_from(sring<NO, NG> &r, const wstream (&w
 
 #define MOE_DOL2_WAVES 8
 
+// The item's NO octets of h staged as stage_octet_lds_z lays them out, by
+// direct global-to-LDS loads (buffer_load ... lds): unit u of a step holds
+// row (u>>2)&7 of the octet, block 2*step + (u&1) and 16-byte piece
+// (u>>5) | ((u>>1)&1)<<1; scale f holds row (f>>1)&7 of block
+// 2*(f>>4) + (f&1).  Of the 32*NO (octet, step) loads wave w issues
+// w*4*NO .. w*4*NO + 4*NO - 1 (all of one octet), and of the 8*NO loads of
+// 64 scales w*NO .. w*NO + NO - 1.  Rows past the item read nothing (their
+// columns are never stored).  For 8 waves and KB == 64.
+template <int NO, int KB>
+__device__ __forceinline__ void stage_octets_dma(const gsrc &src, int row0, int nt, uint32_t *lds, int lane,
+                                                 int wave) {
+  static_assert(KB == 64, "32 steps per octet: 4 per wave and octet");
+  typedef __attribute__((address_space(3))) void *lds_t;
+  constexpr int OW = (int)(octet_lds_bytes_z(KB) / 4);  // dwords per staged octet
+  const int o = (wave * NO) >> 3;
+  const int td = (lane >> 2) & 7, ts = (lane >> 1) & 7;
+  const int sub = (lane >> 5) | (((lane >> 1) & 1) << 1);
+  const uint32_t xo = 8 * o + td < nt ? (uint32_t)(((row0 + 8 * o + td) * KB + (lane & 1)) * (MOE_XSW * 4) + sub * 16)
+                                      : MOE_OOB;
+  const uint32_t so = 8 * o + ts < nt ? (uint32_t)(((row0 + 8 * o + ts) * KB + 2 * (lane >> 4) + (lane & 1)) * 4)
+                                      : MOE_OOB;
+  uint32_t *ol = lds + o * OW;
+#pragma unroll
+  for (int j = 0; j < 4 * NO; j++) {
+    const int st = (wave * 4 * NO + j) & 31;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_t)(ol + st * 65 * 4), 16, xo, 2 * st * (MOE_XSW * 4), 0, 0);
+  }
+#pragma unroll
+  for (int j = 0; j < NO; j++) {
+    const int hh = (wave * NO + j) & 7;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.d, (lds_t)(ol + (KB / 2) * 65 * 4 + hh * 64), 4, so, 8 * hh * 4, 0,
+                                             0);
+  }
+}
+
 // The down work of one wave against NO octets staged at lds (octet o at
 // dword o * octet_lds_bytes(KB) / 4): y of token 8*o + t of the item.
 template <int NQ, int NO>
 __device__ __forceinline__ void dn_ol_octets(const wstream (&ws)[1], const aoff32 &ao, uint32_t *lds,
                                              const uint32_t *__restrict__ hs, const float *__restrict__ hd,
-                                             const int4 &it, const int32_t *__restrict__ perm,
+                                             int n_rows, const int4 &it, const int32_t *__restrict__ perm,
                                              const float *__restrict__ wts, int H, int t32, int lane,
                                              float *__restrict__ y) {
   constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, KB = NQ * 4;
@@ -1046,18 +1092,39 @@ __device__ __forceinline__ void dn_ol_octets(const wstream (&ws)[1], const aoff3
   const int row0 = it.y, nt = it.z;
   const bool shared = it.w != 0;
   sring<NO, NG> r;
-  // first weights in flight during the staging
-  load_sc32<1>(r.sc[0], ws, ao, 0);
+  if constexpr (KB == 64) {
+    // the h loads straight into LDS first, then the first weights, then the
+    // zero slots; the h loads are waited for (vmcnt) right before the barrier
+    stage_octets_dma<NO, KB>(make_gsrc(hs, hd, n_rows, KB), row0, nt, lds, threadIdx.x & 63,
+                             __builtin_amdgcn_readfirstlane(threadIdx.x >> 6));
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    load_sc32<1>(r.sc[0], ws, ao, 0);
 #pragma unroll
-  for (int i = 0; i + 1 < MOE_DRS; i++)
-    if (i < 2 * NQ) load_w32step(r.w[i], ws, ao, i);
+    for (int i = 0; i + 1 < MOE_DRS; i++)
+      if (i < 2 * NQ) load_w32step(r.w[i], ws, ao, i);
 #pragma unroll
-  for (int o = 0; o < NO; o++) {
-    uint32_t *ol = lds + o * OW;
-    stage_octet_lds_z(hs, hd, row0 + 8 * o, nt - 8 * o, KB, reinterpret_cast<u32x4_t *>(ol),
-                      reinterpret_cast<float *>(ol + (KB / 2) * 65 * 4), threadIdx.x, 64 * MOE_DOL2_WAVES);
+    for (int o = 0; o < NO; o++)
+      for (int c = threadIdx.x; c < KB / 2; c += 64 * MOE_DOL2_WAVES)
+        reinterpret_cast<u32x4_t *>(lds + o * OW)[c * 65 + 64] = u32x4_t{0u, 0u, 0u, 0u};
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 + (MOE_DRS - 1 < 2 * NQ ? MOE_DRS - 1 : 2 * NQ)));
+    lds_barrier();
+  } else {
+    // first weights in flight during the staging
+    load_sc32<1>(r.sc[0], ws, ao, 0);
+#pragma unroll
+    for (int i = 0; i + 1 < MOE_DRS; i++)
+      if (i < 2 * NQ) load_w32step(r.w[i], ws, ao, i);
+#pragma unroll
+    for (int o = 0; o < NO; o++) {
+      uint32_t *ol = lds + o * OW;
+      stage_octet_lds_z(hs, hd, row0 + 8 * o, nt - 8 * o, KB, reinterpret_cast<u32x4_t *>(ol),
+                        reinterpret_cast<float *>(ol + (KB / 2) * 65 * 4), threadIdx.x, 64 * MOE_DOL2_WAVES);
+    }
+    __syncthreads();
   }
-  __syncthreads();
   const u32x4_t *bl = reinterpret_cast<const u32x4_t *>(lds);
   const float *dl = reinterpret_cast<const float *>(lds + (KB / 2) * 65 * 4);
   const int n = lane & 31, gb = lane >> 5, t = n >> 2;
@@ -1116,8 +1183,8 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
   const int nt = it.z;
   const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
-  if (nt > 8) dn_ol_octets<NQ, 2>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);  // uniform branch
-  else dn_ol_octets<NQ, 1>(ws, ao, lds, hs, hd, it, perm, wts, H, t32, lane, y);
+  if (nt > 8) dn_ol_octets<NQ, 2>(ws, ao, lds, hs, hd, n_rows, it, perm, wts, H, t32, lane, y);  // uniform branch
+  else dn_ol_octets<NQ, 1>(ws, ao, lds, hs, hd, n_rows, it, perm, wts, H, t32, lane, y);
 }
 
 // ===========================================================================
@@ -1146,16 +1213,6 @@ void k_down_ol2(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs
 #define MOE_GCH_OCT_D (MOE_GCH_STEPS * 16)         // scales per octet per chunk
 #define MOE_GCH_BUF_DW (2 * MOE_GCH_OCT_U4 * 4 + 2 * MOE_GCH_OCT_D)  // dwords per chunk buffer (two octets)
 
-// LDS writes of this wave done, then the workgroup barrier.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// s_waitcnt immediate that waits for vmcnt <= n only (gfx9 encoding: vmcnt
-// in bits 3:0 and 15:14, expcnt 6:4 and lgkmcnt 11:8 left at their maxima).
-__host__ __device__ constexpr int vmcnt_imm(int n) { return (n & 15) | ((n >> 4) << 14) | 0x70 | 0xF00; }
 
 // The staging of a chunk by direct global-to-LDS loads (buffer_load ... lds):
 // a wave's loads write 64 consecutive 16-byte units (one octet's step, lane
