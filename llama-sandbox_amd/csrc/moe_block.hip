@@ -13,6 +13,11 @@
 #include "kernels_group.h"
 #include "kernels_grouped.h"
 #include "kernels_rows.h"
+#include "kernels_stacked.h"
+
+#ifndef MOE_SK
+#define MOE_SK 1  // grouped calls with >= 2 pairs per expert on the stacked-digit kernels
+#endif
 #include "kernels_weights.h"
 
 #include <hip/hip_runtime.h>
@@ -402,6 +407,14 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
   for (const auto &kb : big_lds)
     if (hipFuncSetAttribute(kb.first, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)(2 * octet_lds_bytes_z(kb.second))) != hipSuccess) {
+      delete c;
+      return MOE_ERR_NO_DEVICE;
+    }
+  // and the stacked-digit kernels two chunk buffers of 34 KiB
+  const void *sk_kernels[] = {(const void *)k_gate_up_sk<56>, (const void *)k_gate_up_sk<32>,
+                              (const void *)k_gate_up_sk<16>, (const void *)k_down_sk<16>, (const void *)k_down_sk<8>};
+  for (const void *kf : sk_kernels)
+    if (hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, MOE_SK_LDS_BYTES) != hipSuccess) {
       delete c;
       return MOE_ERR_NO_DEVICE;
     }
@@ -862,12 +875,16 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
   int32_t *items16 = items + group_list_words(T, k, E);
   const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 4 == 0 &&
                   (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
+  // the stacked-digit kernels (items of up to 32 rows) take that list where
+  // down has an instance too
+  const bool sk = MOE_SK && o2 && (F == 128 * 16 || F == 128 * 8) && H % (32 * MOE_SK_WAVES) == 0;
+  const int BT2 = sk ? 32 : 16;
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
   {
     prof_scope pgr(c, K_GROUP, st, s.timed);
     hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
-                       shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, 16,
+                       shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, BT2,
                        o2 ? items16 : (int32_t *)nullptr);
   }
   const int cap = group_item_cap(T, k, E, BT);
@@ -875,8 +892,11 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     prof_scope pg(c, K_GU_GROUPED, st, s.timed);
 #define MOE_GU_ARGS L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
 #define MOE_GU_ARGS16 L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items16, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
-    const dim3 g16(F / (4 * MOE_UNIT), group_item_cap(T, k, E, 16));  // 4 units of F per workgroup
-    if (o2 && H == 128 * 56) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<56, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
+    const dim3 g16(F / (4 * MOE_UNIT), group_item_cap(T, k, E, BT2));  // 4 units of F per workgroup
+    if (sk && H == 128 * 56) hipLaunchKernelGGL(k_gate_up_sk<56>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
+    else if (sk && H == 128 * 32) hipLaunchKernelGGL(k_gate_up_sk<32>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
+    else if (sk && H == 128 * 16) hipLaunchKernelGGL(k_gate_up_sk<16>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
+    else if (o2 && H == 128 * 56) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<56, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
     else if (o2 && H == 128 * 32) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<32, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
     else if (o2 && H == 128 * 16) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<16, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
     else if (oct) hipLaunchKernelGGL(k_gate_up_o, dim3(F / (2 * MOE_UNIT), cap), dim3(256), 0, st, MOE_GU_ARGS);
@@ -893,11 +913,13 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     const size_t lo = octet_lds_bytes(F / MOE_QK), lo2 = 2 * octet_lds_bytes_z(F / MOE_QK);
     // two octets per wave on the 16-row items where that list exists and two
     // workgroups' LDS (2 x 2 staged octets) fit a CU
-    const dim3 gdo2(H / (32 * MOE_DOL2_WAVES), group_item_cap(T, k, E, 16));
+    const dim3 gdo2(H / (32 * MOE_DOL2_WAVES), group_item_cap(T, k, E, BT2));
     const bool dn2 = o2 && H % (32 * MOE_DOL2_WAVES) == 0;
     const dim3 b2(64 * MOE_DOL2_WAVES);
 #define MOE_DN_ARGS16 L.m[T_DOWN].w, s.hq, s.hd, P + T, items16, perm, wts, F, H, s.y
-    if (dn2 && F == 128 * 16) hipLaunchKernelGGL(k_down_ol2<16>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
+    if (sk && F == 128 * 16) hipLaunchKernelGGL(k_down_sk<16>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (sk && F == 128 * 8) hipLaunchKernelGGL(k_down_sk<8>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (dn2 && F == 128 * 16) hipLaunchKernelGGL(k_down_ol2<16>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (dn2 && F == 128 * 8) hipLaunchKernelGGL(k_down_ol2<8>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (dn2 && F == 128 * 6) hipLaunchKernelGGL(k_down_ol2<6>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (oct && F == 128 * 16) hipLaunchKernelGGL(k_down_ol<16>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
