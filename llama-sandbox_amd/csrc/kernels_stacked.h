@@ -32,14 +32,21 @@
 
 #include "kernels_grouped.h"
 
-#define MOE_SK_CH 4                            // quads per staged chunk
+#ifndef MOE_SK_CH
+#define MOE_SK_CH 2                            // quads per staged chunk
+#endif
 #define MOE_SK_STEPS (4 * MOE_SK_CH)           // blocks (MFMA steps) per chunk
 #define MOE_SK_STEP_U4 128                     // 16-byte units per block: [2 halves][64 lanes]
 #define MOE_SK_SC_DW (MOE_SK_STEPS * MOE_SK_STEP_U4 * 4)  // dword offset of the scales in a chunk buffer
 #define MOE_SK_BUF_DW (MOE_SK_SC_DW + MOE_SK_STEPS * 32)  // dwords per chunk buffer (34 KiB)
 #define MOE_SK_LDS_BYTES (2 * MOE_SK_BUF_DW * 4)          // two chunk buffers
 #define MOE_SK_WAVES 8
+#ifndef MOE_SK_RP
 #define MOE_SK_RP 4  // weight ring, in block pairs (3 ahead: 3 KiB in flight per wave)
+#endif
+#ifndef MOE_SK_WPE
+#define MOE_SK_WPE 4  // waves per SIMD the register budget is held to
+#endif
 
 // This lane's staging offsets at block 0 of the staged rows (MOE_OOB: absent
 // token): digits of token lane&31, K half lane>>5; scale of token lane&31,
@@ -55,23 +62,25 @@ __device__ __forceinline__ sdma make_sdma(int lane, int xr, int KB) {
   return s;
 }
 
-// Chunk C of the staged rows into buf: wave w loads blocks 2w and 2w+1 (both
-// halves) and the scales of blocks 2w, 2w+1: 5 loads per wave.
+// Chunk C of the staged rows into buf: wave w loads the blocks w*SW ..
+// w*SW + SW - 1 of the chunk (both halves; SW = blocks per wave) and the
+// scales of two blocks (waves below MOE_SK_STEPS/2): 2*SW + 1 loads or 2*SW.
+#define MOE_SK_SW (MOE_SK_STEPS / MOE_SK_WAVES)
 template <int C>
 __device__ __forceinline__ void sdma_issue(const sdma &g, const gsrc &src, uint32_t *buf, int wave) {
   typedef __attribute__((address_space(3))) void *lds_t;
 #pragma unroll
-  for (int i = 0; i < 2; i++) {
-    const int st = 2 * wave + i;
+  for (int i = 0; i < MOE_SK_SW; i++) {
+    const int st = MOE_SK_SW * wave + i;
 #pragma unroll
     for (int h = 0; h < 2; h++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_t)(buf + (st * 2 + h) * 64 * 4), 16, g.xo,
                                                (MOE_SK_STEPS * C + st) * (MOE_XSW * 4) + h * 32, 0, 0);
   }
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(src.d, (lds_t)(buf + MOE_SK_SC_DW + 2 * wave * 32), 4, g.so,
-                                           (MOE_SK_STEPS * C + 2 * wave) * 4, 0, 0);
+  if (wave < MOE_SK_STEPS / 2)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(src.d, (lds_t)(buf + MOE_SK_SC_DW + 2 * wave * 32), 4, g.so,
+                                             (MOE_SK_STEPS * C + 2 * wave) * 4, 0, 0);
 }
-#define MOE_SK_DMA_LOADS 5
 
 // One block's B operand and d of this lane, from a chunk buffer.
 struct skb {
@@ -118,9 +127,11 @@ struct skring {
 template <int C, int NQ>
 __host__ __device__ constexpr int sdma_after() {
   int n = 0;
-  if (C + 1 < NQ / MOE_SK_CH) n += 2;
-  for (int p = 0; p < 2 * MOE_SK_CH; p++)
-    if (2 * MOE_SK_CH * C + p + MOE_SK_RP - 1 < 2 * NQ) n++;
+  for (int q = MOE_SK_CH * C; q < MOE_SK_CH * (C + 1); q++) {
+    if ((q & 3) == 0 && q / 4 + 1 < NQ / 4) n += 2;  // the next group's exponent dwords
+    for (int j = 0; j < 2; j++)
+      if (2 * q + j + MOE_SK_RP - 1 < 2 * NQ) n++;  // weight pairs
+  }
   return n;
 }
 
@@ -227,7 +238,7 @@ __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao
 // threads, LDS MOE_SK_LDS_BYTES.  Requires H == 128 * NQ, NQ % 4 == 0,
 // (F/32) % 4 == 0.
 template <int NQ>
-__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(MOE_SK_WPE)))
 void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
                   const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                   int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
@@ -277,7 +288,7 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
 // capacity), 512 threads, LDS MOE_SK_LDS_BYTES.  Requires F == 128 * NQ,
 // NQ % 4 == 0, H % 256 == 0.
 template <int NQ>
-__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(MOE_SK_WPE)))
 void k_down_sk(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
                int n_rows, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                const float *__restrict__ wts, int F, int H, float *__restrict__ y) {

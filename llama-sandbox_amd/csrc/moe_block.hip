@@ -18,6 +18,9 @@
 #ifndef MOE_SK
 #define MOE_SK 1  // grouped calls with >= 2 pairs per expert on the stacked-digit kernels
 #endif
+#ifndef MOE_SK_ALL
+#define MOE_SK_ALL 0  // ... and every grouped call whose shape they take
+#endif
 #include "kernels_weights.h"
 
 #include <hip/hip_runtime.h>
@@ -877,7 +880,9 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
                   (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
   // the stacked-digit kernels (items of up to 32 rows) take that list where
   // down has an instance too
-  const bool sk = MOE_SK && o2 && (F == 128 * 16 || F == 128 * 8) && H % (32 * MOE_SK_WAVES) == 0;
+  const bool sk_shape = MOE_SK && (F == 128 * 16 || F == 128 * 8) && H % (32 * MOE_SK_WAVES) == 0 &&
+                        (F / MOE_UNIT) % 4 == 0 && (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
+  const bool sk = sk_shape && (MOE_SK_ALL ? T > 1 : o2);
   const int BT2 = sk ? 32 : 16;
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
@@ -885,7 +890,7 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     prof_scope pgr(c, K_GROUP, st, s.timed);
     hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
                        shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, BT2,
-                       o2 ? items16 : (int32_t *)nullptr);
+                       (o2 || sk) ? items16 : (int32_t *)nullptr);
   }
   const int cap = group_item_cap(T, k, E, BT);
   {
