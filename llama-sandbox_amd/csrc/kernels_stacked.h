@@ -50,15 +50,20 @@
 
 // This lane's staging offsets at block 0 of the staged rows (MOE_OOB: absent
 // token): digits of token lane&31, K half lane>>5; scale of token lane&31,
-// block lane>>5.
+// block lane>>5.  The staged rows are row-major ([row][block], x) or
+// block-major ([block][row], the h rows these kernels write): bs / bs4 =
+// bytes from one block to the next of a row, digits / scales.
 struct sdma {
-  uint32_t xo, so;
+  uint32_t xo, so, bs, bs4;
 };
 
-__device__ __forceinline__ sdma make_sdma(int lane, int xr, int KB) {
+__device__ __forceinline__ sdma make_sdma(int lane, int xr, int KB, bool block_major, int n_rows) {
   sdma s;
-  s.xo = xr >= 0 ? (uint32_t)xr * KB * (MOE_XSW * 4) + (uint32_t)(lane >> 5) * 16 : MOE_OOB;
-  s.so = xr >= 0 ? ((uint32_t)xr * KB + (uint32_t)(lane >> 5)) * 4 : MOE_OOB;
+  const uint32_t rs = block_major ? MOE_XSW * 4 : (uint32_t)KB * MOE_XSW * 4, rs4 = block_major ? 4 : (uint32_t)KB * 4;
+  s.bs = block_major ? (uint32_t)n_rows * MOE_XSW * 4 : MOE_XSW * 4;
+  s.bs4 = block_major ? (uint32_t)n_rows * 4 : 4;
+  s.xo = xr >= 0 ? (uint32_t)xr * rs + (uint32_t)(lane >> 5) * 16 : MOE_OOB;
+  s.so = xr >= 0 ? (uint32_t)xr * rs4 + (uint32_t)(lane >> 5) * s.bs4 : MOE_OOB;
   return s;
 }
 
@@ -75,11 +80,11 @@ __device__ __forceinline__ void sdma_issue(const sdma &g, const gsrc &src, uint3
 #pragma unroll
     for (int h = 0; h < 2; h++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(src.x, (lds_t)(buf + (st * 2 + h) * 64 * 4), 16, g.xo,
-                                               (MOE_SK_STEPS * C + st) * (MOE_XSW * 4) + h * 32, 0, 0);
+                                               (MOE_SK_STEPS * C + st) * g.bs + h * 32, 0, 0);
   }
   if (wave < MOE_SK_STEPS / 2)
     __builtin_amdgcn_raw_ptr_buffer_load_lds(src.d, (lds_t)(buf + MOE_SK_SC_DW + 2 * wave * 32), 4, g.so,
-                                             (MOE_SK_STEPS * C + 2 * wave) * 4, 0, 0);
+                                             (MOE_SK_STEPS * C + 2 * wave) * g.bs4, 0, 0);
 }
 
 // One block's B operand and d of this lane, from a chunk buffer.
@@ -208,9 +213,10 @@ __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1
 // acc: lane n + 32*gb, element 4i + j = token n, row 8i + 4gb + j.
 template <int NQ>
 __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src, int xr, int KB,
-                                        uint32_t *lds, int wave, int lane, f32x16_t &acc) {
+                                        bool block_major, int n_rows, uint32_t *lds, int wave, int lane,
+                                        f32x16_t &acc) {
   static_assert(NQ % MOE_SK_CH == 0, "whole chunks");
-  const sdma g = make_sdma(lane, xr, KB);
+  const sdma g = make_sdma(lane, xr, KB, block_major, n_rows);
   skring<NQ / 4> r;
   sdma_issue<0>(g, src, lds, wave);
   asm volatile("" ::: "memory");
@@ -247,9 +253,9 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   if ((int)blockIdx.y >= items[0]) return;
   const int4 it = item_of(items, blockIdx.y);
   constexpr int NQ4 = NQ / 4, KB = NQ * 4;
-  const int U = F / MOE_UNIT, tiles = F / MOE_TILE;
+  const int tiles = F / MOE_TILE;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int P = T * k, row0 = it.y, nt = it.z;
+  const int P = T * k, NR = P + T, row0 = it.y, nt = it.z;
   const bool shared = it.w != 0;
   const int u = 4 * blockIdx.x + (wave & 3);
   const wstream ws[1] = {make_wstream32(wave >= 4 ? w_u : w_g, (size_t)it.x * tiles + 2 * u, NQ4)};
@@ -258,7 +264,7 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const int n = lane & 31, gb = lane >> 5;
   const int xr = n < nt ? (shared ? row0 + n - P : perm[row0 + n] / k) : -1;
   f32x16_t acc;
-  sk_loop<NQ>(ws, ao, src, xr, KB, lds, wave, lane, acc);
+  sk_loop<NQ>(ws, ao, src, xr, KB, false, T, lds, wave, lane, acc);
   lds_barrier();  // every wave is done with the chunk buffers
   float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
@@ -276,7 +282,8 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
     const float usum = red[((ul * 2 + 1) * 32 + t) * MOE_UNIT + j];
     const float h = live ? swiglu(gsum, usum, clamp) : 0.0f;
     const int hrow = row0 + (live ? t : 0), uu = 4 * blockIdx.x + ul;
-    h_unit_store(h, live, hs + ((size_t)hrow * U + uu) * MOE_XSW, hd + (size_t)hrow * U + uu, lane);
+    // h block-major ([unit of F][grouped row]): an item's rows of one unit are adjacent
+    h_unit_store(h, live, hs + ((size_t)uu * NR + hrow) * MOE_XSW, hd + (size_t)uu * NR + hrow, lane);
     if (htap && live) htap[(size_t)hrow * F + (size_t)uu * MOE_UNIT + j] = h;
   }
 }
@@ -307,7 +314,7 @@ void k_down_sk(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   const int n = lane & 31, gb = lane >> 5;
   const bool live = n < nt;
   f32x16_t acc;
-  sk_loop<NQ>(ws, ao, src, live ? row0 + n : -1, KB, lds, wave, lane, acc);
+  sk_loop<NQ>(ws, ao, src, live ? row0 + n : -1, KB, true, n_rows, lds, wave, lane, acc);
   const int rr = row0 + (live ? n : 0);
   const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
   float v[16];
