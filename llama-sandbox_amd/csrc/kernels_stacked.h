@@ -32,21 +32,14 @@
 
 #include "kernels_grouped.h"
 
-#ifndef MOE_SK_CH
-#define MOE_SK_CH 2                            // quads per staged chunk
-#endif
+#define MOE_SK_CH 2                            // quads per staged chunk (4: 16 blocks, 100 VGPRs, measured 2% slower)
 #define MOE_SK_STEPS (4 * MOE_SK_CH)           // blocks (MFMA steps) per chunk
 #define MOE_SK_STEP_U4 128                     // 16-byte units per block: [2 halves][64 lanes]
 #define MOE_SK_SC_DW (MOE_SK_STEPS * MOE_SK_STEP_U4 * 4)  // dword offset of the scales in a chunk buffer
 #define MOE_SK_BUF_DW (MOE_SK_SC_DW + MOE_SK_STEPS * 32)  // dwords per chunk buffer (34 KiB)
 #define MOE_SK_LDS_BYTES (2 * MOE_SK_BUF_DW * 4)          // two chunk buffers
 #define MOE_SK_WAVES 8
-#ifndef MOE_SK_RP
-#define MOE_SK_RP 4  // weight ring, in block pairs (3 ahead: 3 KiB in flight per wave)
-#endif
-#ifndef MOE_SK_WPE
-#define MOE_SK_WPE 4  // waves per SIMD the register budget is held to
-#endif
+#define MOE_SK_RP 4  // weight ring, in block pairs (3 ahead: 3 KiB in flight per wave; 2 and 5 ahead measured the same)
 
 // This lane's staging offsets at block 0 of the staged rows (MOE_OOB: absent
 // token): digits of token lane&31, K half lane>>5; scale of token lane&31,
@@ -244,7 +237,7 @@ __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao
 // threads, LDS MOE_SK_LDS_BYTES.  Requires H == 128 * NQ, NQ % 4 == 0,
 // (F/32) % 4 == 0.
 template <int NQ>
-__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(MOE_SK_WPE)))
+__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
 void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const uint32_t *__restrict__ xq,
                   const float *__restrict__ xd, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                   int k, int T, int F, int H, float clamp, uint32_t *__restrict__ hs, float *__restrict__ hd,
@@ -295,7 +288,7 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
 // capacity), 512 threads, LDS MOE_SK_LDS_BYTES.  Requires F == 128 * NQ,
 // NQ % 4 == 0, H % 256 == 0.
 template <int NQ>
-__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(MOE_SK_WPE)))
+__global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
 void k_down_sk(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
                int n_rows, const int32_t *__restrict__ items, const int32_t *__restrict__ perm,
                const float *__restrict__ wts, int F, int H, float *__restrict__ y) {

@@ -15,12 +15,6 @@
 #include "kernels_rows.h"
 #include "kernels_stacked.h"
 
-#ifndef MOE_SK
-#define MOE_SK 1  // grouped calls with >= 2 pairs per expert on the stacked-digit kernels
-#endif
-#ifndef MOE_SK_ALL
-#define MOE_SK_ALL 0  // ... and every grouped call whose shape they take
-#endif
 #include "kernels_weights.h"
 
 #include <hip/hip_runtime.h>
@@ -404,9 +398,7 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
   c->budget = (inject & 2) ? 0 : budget_bytes;
   c->inject = inject;
   // the two-octet down kernels stage more than 64 KiB of LDS per workgroup
-  const std::pair<const void *, int> big_lds[] = {{(const void *)k_down_ol2<16>, 16 * 4},
-                                                  {(const void *)k_down_ol2<8>, 8 * 4},
-                                                  {(const void *)k_down_ol2<6>, 6 * 4}};
+  const std::pair<const void *, int> big_lds[] = {{(const void *)k_down_ol2<6>, 6 * 4}};
   for (const auto &kb : big_lds)
     if (hipFuncSetAttribute(kb.first, hipFuncAttributeMaxDynamicSharedMemorySize,
                             (int)(2 * octet_lds_bytes_z(kb.second))) != hipSuccess) {
@@ -871,18 +863,17 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
   const bool oct = use_octets(T);
   const int BT = oct ? 8 : 4;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
-  // octets: where the shape has an instance and the batch averages 2 pairs
-  // per expert or more, gate/up (k_gate_up_ol) and down (k_down_ol2) run on
-  // a second list of items of up to 16 rows, B staged in LDS; below that most
-  // items hold one octet and the 8-row list with B from global memory is used
+  // where the shape has an instance and the batch averages 2 pairs per
+  // expert or more, gate/up and down run on a second item list with B staged
+  // in LDS: items of up to 32 rows on the stacked-digit kernels
+  // (k_gate_up_sk / k_down_sk, F = 128 * {16, 8}), else items of up to 16 rows
+  // on the octet kernels (k_gate_up_ol / k_down_ol2); below 2 pairs per
+  // expert most items hold one octet and the 8-row list with B from global
+  // memory is used
   int32_t *items16 = items + group_list_words(T, k, E);
   const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 4 == 0 &&
                   (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
-  // the stacked-digit kernels (items of up to 32 rows) take that list where
-  // down has an instance too
-  const bool sk_shape = MOE_SK && (F == 128 * 16 || F == 128 * 8) && H % (32 * MOE_SK_WAVES) == 0 &&
-                        (F / MOE_UNIT) % 4 == 0 && (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
-  const bool sk = sk_shape && (MOE_SK_ALL ? T > 1 : o2);
+  const bool sk = o2 && (F == 128 * 16 || F == 128 * 8);
   const int BT2 = sk ? 32 : 16;
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
@@ -917,15 +908,14 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     const dim3 gdo(H / 128, cap);
     const size_t lo = octet_lds_bytes(F / MOE_QK), lo2 = 2 * octet_lds_bytes_z(F / MOE_QK);
     // two octets per wave on the 16-row items where that list exists and two
-    // workgroups' LDS (2 x 2 staged octets) fit a CU
+    // workgroups' LDS (2 x 2 staged octets) fit a CU (F = 768; the stacked
+    // kernels take F = 1024 and 2048)
     const dim3 gdo2(H / (32 * MOE_DOL2_WAVES), group_item_cap(T, k, E, BT2));
     const bool dn2 = o2 && H % (32 * MOE_DOL2_WAVES) == 0;
     const dim3 b2(64 * MOE_DOL2_WAVES);
 #define MOE_DN_ARGS16 L.m[T_DOWN].w, s.hq, s.hd, P + T, items16, perm, wts, F, H, s.y
     if (sk && F == 128 * 16) hipLaunchKernelGGL(k_down_sk<16>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
     else if (sk && F == 128 * 8) hipLaunchKernelGGL(k_down_sk<8>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
-    else if (dn2 && F == 128 * 16) hipLaunchKernelGGL(k_down_ol2<16>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
-    else if (dn2 && F == 128 * 8) hipLaunchKernelGGL(k_down_ol2<8>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (dn2 && F == 128 * 6) hipLaunchKernelGGL(k_down_ol2<6>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (oct && F == 128 * 16) hipLaunchKernelGGL(k_down_ol<16>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
     else if (oct && F == 128 * 6) hipLaunchKernelGGL(k_down_ol<6>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
