@@ -361,6 +361,7 @@ SWEEP = [
     (7168, 768, 8, 4, 40, False, 5.0, wl.ROUTE_SOFTMAX),      # k_down_ol2<6>, 16 + 4-row items, clamp
     (2048, 2048, 16, 4, 24, True, 0.0, wl.ROUTE_SIGMOID),     # stacked: k_gate_up_sk<16>, k_down_sk<16>
     (2048, 1024, 8, 4, 80, False, 3.0, wl.ROUTE_SOFTMAX),     # stacked, experts of 32 + n rows, clamp
+    (4096, 1536, 16, 4, 32, True, 0.0, wl.ROUTE_SIGMOID),     # ol<32> (F without a stacked instance), k_down_o
 ]
 
 
