@@ -23,11 +23,14 @@
 // The B scale of lane n + 32*gb is that of K block gb (hi: 2^4, lo: 2^0).
 // D lane n + 32*gb holds column n, rows 8*i + 4*gb + j at element 4*i + j.
 //
-// B is staged in LDS by chunks of MOE_SK_CH quads (16 blocks), double
+// B is staged in LDS by chunks of MOE_SK_CH quads (8 blocks), double
 // buffered, with direct global-to-LDS loads: per block, two 1 KiB runs (the
 // 64 lanes' bytes 0-15, then bytes 16-31, each lane 16 consecutive bytes,
 // so the operand reads are conflict-free), then the chunk's scales
 // [block][32 tokens].  An absent token reads zeros (out-of-range offset).
+// The x rows are read from the grouped chain's staged x; the h rows that
+// k_gate_up_sk writes for k_down_sk are block-major, so the 32 rows of an
+// item are adjacent for each block.
 #pragma once
 
 #include "kernels_grouped.h"
@@ -38,7 +41,7 @@
 #define MOE_SK_SC_DW (MOE_SK_STEPS * MOE_SK_STEP_U4 * 4)  // dword offset of the scales in a chunk buffer
 #define MOE_SK_BUF_DW (MOE_SK_SC_DW + MOE_SK_STEPS * 32)  // dwords per chunk buffer (34 KiB)
 #define MOE_SK_LDS_BYTES (2 * MOE_SK_BUF_DW * 4)          // two chunk buffers
-#define MOE_SK_WAVES 8
+#define MOE_SK_WAVES 8                          // waves per workgroup (one 32-row weight tile each)
 #define MOE_SK_RP 4  // weight ring, in block pairs (3 ahead: 3 KiB in flight per wave; 2 and 5 ahead measured the same)
 
 // This lane's staging offsets at block 0 of the staged rows (MOE_OOB: absent
