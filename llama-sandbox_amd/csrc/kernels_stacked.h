@@ -39,8 +39,8 @@
 #define MOE_SK_STEPS (4 * MOE_SK_CH)           // blocks (MFMA steps) per chunk
 #define MOE_SK_STEP_U4 128                     // 16-byte units per block: [2 halves][64 lanes]
 #define MOE_SK_SC_DW (MOE_SK_STEPS * MOE_SK_STEP_U4 * 4)  // dword offset of the scales in a chunk buffer
-#define MOE_SK_BUF_DW (MOE_SK_SC_DW + MOE_SK_STEPS * 32)  // dwords per chunk buffer (34 KiB)
-#define MOE_SK_LDS_BYTES (2 * MOE_SK_BUF_DW * 4)          // two chunk buffers
+#define MOE_SK_BUF_DW (MOE_SK_SC_DW + MOE_SK_STEPS * 32)  // dwords per chunk buffer (17 KiB)
+#define MOE_SK_LDS_BYTES (2 * MOE_SK_BUF_DW * 4)          // two chunk buffers (34 KiB)
 #define MOE_SK_WAVES 8                          // waves per workgroup (one 32-row weight tile each)
 #define MOE_SK_RP 4  // weight ring, in block pairs (3 ahead: 3 KiB in flight per wave; 2 and 5 ahead measured the same)
 

@@ -405,7 +405,7 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
       delete c;
       return MOE_ERR_NO_DEVICE;
     }
-  // and the stacked-digit kernels two chunk buffers of 34 KiB
+  // and the stacked-digit kernels (two 17 KiB chunk buffers, 34 KiB; set for uniformity)
   const void *sk_kernels[] = {(const void *)k_gate_up_sk<56>, (const void *)k_gate_up_sk<32>,
                               (const void *)k_gate_up_sk<16>, (const void *)k_down_sk<16>, (const void *)k_down_sk<8>};
   for (const void *kf : sk_kernels)
