@@ -22,6 +22,10 @@ typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
 
 #define MOE_QK 32
 
+// Flags of a work item (k_group's item records, word 3).
+#define MOE_ITEM_SHARED 1  // the shared expert's rows
+#define MOE_ITEM_SPLIT 2   // the expert's rows span more than one item (its tiles are read again)
+
 // 2^(e-127) * d, exact whenever the result is a normal f32.
 __device__ __forceinline__ float scale_e8m0(float d, uint32_t e) {
   return __builtin_amdgcn_ldexpf(d, (int)e - 127);

@@ -54,8 +54,9 @@ __device__ __forceinline__ uint64_t same_id_lanes(int e, bool valid) {
 //   pass 1: per-wave counts wc[w][e] (one writer per expert per step);
 //   then the histogram (sum over waves), exclusive scans over experts of
 //   the counts and of the item counts ceil(c_e / BT), the item list
-//   (items != NULL: {expert, first row, rows, 0} per item in expert order,
-//   then the shared expert's {E, P + j*BT, rows, 1} when `shared`), and
+//   (items != NULL: {expert, first row, rows, flags} per item in expert
+//   order, then the shared expert's {E, P + j*BT, rows, flags} when
+//   `shared`; flags: MOE_ITEM_SHARED, MOE_ITEM_SPLIT), and
 //   wc[w][e] turned into wave w's first row of expert e;
 //   pass 2: row of a pair = wc[w][e] + rank, so rows ascend in pair order
 //   within each expert (ggml mul_mat_id's order).
@@ -161,12 +162,12 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     int4 *rec = items ? reinterpret_cast<int4 *>(items) + 1 + excli : nullptr;
     for (int j = 0; j < ni; j++) {
       const int r = j * BT;
-      rec[j] = make_int4(tid, excl + r, c - r < BT ? c - r : BT, 0);
+      rec[j] = make_int4(tid, excl + r, c - r < BT ? c - r : BT, ni > 1 ? MOE_ITEM_SPLIT : 0);
     }
     int4 *rec2 = items2 ? reinterpret_cast<int4 *>(items2) + 1 + excli2 : nullptr;
     for (int j = 0; j < ni2; j++) {
       const int r = j * BT2;
-      rec2[j] = make_int4(tid, excl + r, c - r < BT2 ? c - r : BT2, 0);
+      rec2[j] = make_int4(tid, excl + r, c - r < BT2 ? c - r : BT2, ni2 > 1 ? MOE_ITEM_SPLIT : 0);
     }
   }
   if (tid == 1023) {  // thread 1023's inclusive sums are the totals
@@ -179,7 +180,8 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     const int ns = shared ? (T + BT - 1) / BT : 0;
     for (int j = tid; j < ns; j += 1024) {
       const int r = j * BT;
-      reinterpret_cast<int4 *>(items)[1 + tot[0] + j] = make_int4(E, P + r, T - r < BT ? T - r : BT, 1);
+      reinterpret_cast<int4 *>(items)[1 + tot[0] + j] =
+          make_int4(E, P + r, T - r < BT ? T - r : BT, MOE_ITEM_SHARED | (ns > 1 ? MOE_ITEM_SPLIT : 0));
     }
     if (tid == 0) items[0] = tot[0] + ns;
   }
@@ -187,7 +189,8 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
     const int ns = shared ? (T + BT2 - 1) / BT2 : 0;
     for (int j = tid; j < ns; j += 1024) {
       const int r = j * BT2;
-      reinterpret_cast<int4 *>(items2)[1 + tot[1] + j] = make_int4(E, P + r, T - r < BT2 ? T - r : BT2, 1);
+      reinterpret_cast<int4 *>(items2)[1 + tot[1] + j] =
+          make_int4(E, P + r, T - r < BT2 ? T - r : BT2, MOE_ITEM_SHARED | (ns > 1 ? MOE_ITEM_SPLIT : 0));
     }
     if (tid == 0) items2[0] = tot[1] + ns;
   }

@@ -29,8 +29,9 @@
 
 #define MOE_OOB 0x80000000u  // a buffer offset past any staged buffer: the load returns 0
 
-// Item record written by k_group: {matrix, first grouped row, rows, shared}.
-// items[0] = number of items; record i is int4 number 1 + i.
+// Item record written by k_group: {matrix, first grouped row, rows, flags
+// (MOE_ITEM_SHARED, MOE_ITEM_SPLIT)}.  items[0] = number of items; record i
+// is int4 number 1 + i.
 __device__ __forceinline__ int4 item_of(const int32_t *__restrict__ items, int i) {
   return reinterpret_cast<const int4 *>(items)[1 + i];
 }
@@ -251,7 +252,7 @@ __device__ __forceinline__ void gu_item(const uint8_t *__restrict__ w_g, const u
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int ti = wave & 1, kp = wave >> 1, P = T * k, u = blockIdx.x;
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   int q0, q1;
   wave_quads(NQ, 2, kp, q0, q1);
   const size_t t0 = (size_t)it.x * tiles + 2 * u + ti;
@@ -265,7 +266,9 @@ __device__ __forceinline__ void gu_item(const uint8_t *__restrict__ w_g, const u
     gs[p] = make_gsel(lane, xr, KB);
   }
   f32x4_t acc[NP][2];
-  gloop_any<2, NP, 0>(ws, q0, q1, src, gs, lane, acc);
+  // the pairs path runs for T <= 4: an expert has at most T rows, so one item
+  // and every weight tile is read once per call (non-temporal, as in decode)
+  gloop_any<2, NP, MOE_CPOL_NT>(ws, q0, q1, src, gs, lane, acc);
   const int gb = lane >> 4, tp = (lane >> 3) & 1;
 #pragma unroll
   for (int p = 0; p < NP; p++)
@@ -331,7 +334,7 @@ __device__ __forceinline__ void dn_item(const uint8_t *__restrict__ w_d, const g
   const int pair = blockIdx.x * MOE_DG_WAVES + wave;  // tiles 2*pair, 2*pair + 1
   if (2 * pair >= tiles) return;
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   const size_t t0 = (size_t)it.x * tiles + 2 * pair;
   const wstream ws[2] = {make_wstream(w_d, t0, NQ4), make_wstream(w_d, t0 + 1, NQ4)};
   gsel gs[NP];
@@ -341,7 +344,7 @@ __device__ __forceinline__ void dn_item(const uint8_t *__restrict__ w_d, const g
     gs[p] = make_gsel(lane, i < nt ? row0 + i : -1, KB);
   }
   f32x4_t acc[NP][2];
-  gloop_any<2, NP, 0>(ws, 0, NQ, src, gs, lane, acc);
+  gloop_any<2, NP, MOE_CPOL_NT>(ws, 0, NQ, src, gs, lane, acc);  // one item per expert (T <= 4): read once
   const int gb = lane >> 4, tp = (lane >> 3) & 1;
 #pragma unroll
   for (int p = 0; p < NP; p++) {
@@ -651,7 +654,7 @@ void k_gate_up_o(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_
   const int ul = wave & 1, kp = wave >> 1, P = T * k;
   const int u = 2 * blockIdx.x + ul;
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   int q0, q1;
   wave_quads(NQ, 2, kp, q0, q1);
   const size_t t0 = (size_t)it.x * tiles + 2 * u;
@@ -706,7 +709,7 @@ void k_down_o(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, 
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t32 = blockIdx.x * 4 + wave;  // 32-row tile of H
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
   const gsrc src = make_gsrc(hs, hd, n_rows, KB);
@@ -853,7 +856,7 @@ void k_down_ol(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int t32 = blockIdx.x * 4 + wave;  // 32-row tile of H
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
   oring_l<1, 1, NG> r;
@@ -985,10 +988,12 @@ __device__ __forceinline__ void step_scale(const stepres<NO> &res, const float (
   for (int o = 0; o < NO; o++) asm volatile("" : "+v"(acc[o][0]));
 }
 
-// One step's weights (step S = 2 * quad + j of the stream).
+// One step's weights (step S = 2 * quad + j of the stream), cache policy CPOL.
+template <int CPOL = 0>
 __device__ __forceinline__ void load_w32step(u32x4_t &w, const wstream (&ws)[1], const aoff32 &ao, int S) {
   const int q = S >> 1, j = S & 1;
-  w = __builtin_amdgcn_raw_buffer_load_b128(ws[0].rec, ao.v + j * 512, (q >> 2) * MOE_REC_BYTES + (q & 3) * 1024, 0);
+  w = __builtin_amdgcn_raw_buffer_load_b128(ws[0].rec, ao.v + j * 512, (q >> 2) * MOE_REC_BYTES + (q & 3) * 1024,
+                                            CPOL);
 }
 
 #define MOE_DRS 4  // weight ring of the down step loop, in steps
@@ -1090,7 +1095,7 @@ __device__ __forceinline__ void dn_ol_octets(const wstream (&ws)[1], const aoff3
   constexpr int NQ4 = (NQ + 3) / 4, NG = NQ4, KB = NQ * 4;
   constexpr int OW = (int)(octet_lds_bytes_z(KB) / 4);  // dwords per staged octet
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   sring<NO, NG> r;
   if constexpr (KB == 64) {
     // the h loads straight into LDS first, then the first weights, then the
@@ -1429,7 +1434,7 @@ void k_gate_up_ol(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const int U = F / MOE_UNIT, tiles = F / MOE_TILE;
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int P = T * k, row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   const int u = NU * blockIdx.x + wave % NU;
   const wstream ws[1] = {make_wstream32(wave >= NU ? w_u : w_g, (size_t)it.x * tiles + 2 * u, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);

@@ -158,8 +158,8 @@ __device__ __forceinline__ void sk_step(const u32x4_t &a4, uint32_t sa, skb &b, 
   if (next) load_skb_d(b, nbuf, lane, nst);
 }
 
-// Quads QL .. NQ-1 of the K loop.
-template <int QL, int NQ>
+// Quads QL .. NQ-1 of the K loop (weights loaded with cache policy CPOL).
+template <int QL, int NQ, int CPOL>
 __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1], const aoff32 &ao,
                                         const gsrc &src, const sdma &g, uint32_t *lds, int wave, int lane, int sb,
                                         f32x16_t &acc) {
@@ -180,7 +180,7 @@ __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1
 #pragma unroll
     for (int j = 0; j < 2; j++) {
       const int P = 2 * QL + j;
-      if (P + RP - 1 < 2 * NQ) load_w32step(r.w[(P + RP - 1) % RP], ws, ao, P + RP - 1);
+      if (P + RP - 1 < 2 * NQ) load_w32step<CPOL>(r.w[(P + RP - 1) % RP], ws, ao, P + RP - 1);
       asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
       u32x4_t a0, a1;
@@ -200,14 +200,15 @@ __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1
       load_skb_v(r.b, nb, lane, 0);
       load_skb_d(r.b, nb, lane, 0);
     }
-    sk_from<QL + 1, NQ>(r, ws, ao, src, g, lds, wave, lane, sb, acc);
+    sk_from<QL + 1, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, sb, acc);
   }
 }
 
 // The K loop of one wave: its 32-row weight tile over NQ quads against the
 // 32 staged tokens (xr: the staged row of token lane&31, < 0 absent).
-// acc: lane n + 32*gb, element 4i + j = token n, row 8i + 4gb + j.
-template <int NQ>
+// acc: lane n + 32*gb, element 4i + j = token n, row 8i + 4gb + j.  CPOL:
+// the weights' cache policy (non-temporal where no other item reads them).
+template <int NQ, int CPOL>
 __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src, int xr, int KB,
                                         bool block_major, int n_rows, uint32_t *lds, int wave, int lane,
                                         f32x16_t &acc) {
@@ -220,7 +221,7 @@ __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao
   load_sc32<1>(r.sc[0], ws, ao, 0);
 #pragma unroll
   for (int i = 0; i + 1 < MOE_SK_RP; i++)
-    if (i < 2 * NQ) load_w32step(r.w[i], ws, ao, i);
+    if (i < 2 * NQ) load_w32step<CPOL>(r.w[i], ws, ao, i);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
   // chunk 0 has landed (2 exponent dwords and the first weight pairs went out after it)
@@ -230,7 +231,7 @@ __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao
   for (int e = 0; e < 16; e++) acc[e] = 0.0f;
   load_skb_v(r.b, lds, lane, 0);
   load_skb_d(r.b, lds, lane, 0);
-  sk_from<0, NQ>(r, ws, ao, src, g, lds, wave, lane, (lane >> 5) ? 127 : 131, acc);
+  sk_from<0, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, (lane >> 5) ? 127 : 131, acc);
 }
 
 // gate/up -> clamp -> SwiGLU -> Q8_0(h) on items of up to 32 rows.  One
@@ -252,7 +253,7 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const int tiles = F / MOE_TILE;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int P = T * k, NR = P + T, row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   const int u = 4 * blockIdx.x + (wave & 3);
   const wstream ws[1] = {make_wstream32(wave >= 4 ? w_u : w_g, (size_t)it.x * tiles + 2 * u, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
@@ -260,7 +261,10 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const int n = lane & 31, gb = lane >> 5;
   const int xr = n < nt ? (shared ? row0 + n - P : perm[row0 + n] / k) : -1;
   f32x16_t acc;
-  sk_loop<NQ>(ws, ao, src, xr, KB, false, T, lds, wave, lane, acc);
+  // an expert of one item reads its tiles once: non-temporal, as in decode;
+  // the items of a larger expert share them through L2
+  if (it.w & MOE_ITEM_SPLIT) sk_loop<NQ, 0>(ws, ao, src, xr, KB, false, T, lds, wave, lane, acc);
+  else sk_loop<NQ, MOE_CPOL_NT>(ws, ao, src, xr, KB, false, T, lds, wave, lane, acc);
   lds_barrier();  // every wave is done with the chunk buffers
   float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
@@ -302,7 +306,7 @@ void k_down_sk(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   const int tiles = H / MOE_TILE;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int row0 = it.y, nt = it.z;
-  const bool shared = it.w != 0;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
   const int t32 = blockIdx.x * MOE_SK_WAVES + wave;  // 32-row tile of H
   const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
@@ -310,7 +314,8 @@ void k_down_sk(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   const int n = lane & 31, gb = lane >> 5;
   const bool live = n < nt;
   f32x16_t acc;
-  sk_loop<NQ>(ws, ao, src, live ? row0 + n : -1, KB, true, n_rows, lds, wave, lane, acc);
+  if (it.w & MOE_ITEM_SPLIT) sk_loop<NQ, 0>(ws, ao, src, live ? row0 + n : -1, KB, true, n_rows, lds, wave, lane, acc);
+  else sk_loop<NQ, MOE_CPOL_NT>(ws, ao, src, live ? row0 + n : -1, KB, true, n_rows, lds, wave, lane, acc);
   const int rr = row0 + (live ? n : 0);
   const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
   float v[16];
