@@ -669,7 +669,9 @@ void k_gate_up_o(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_
     gs[0] = make_gsel32(lane, xr, KB);
   }
   f32x16_t acc[1][2];
-  oloop_any<2, 1, 0>(ws, ao, q0, q1, src, gs, lane, acc);
+  // non-temporal weights where no other item of the expert reads them
+  if (it.w & MOE_ITEM_SPLIT) oloop_any<2, 1, 0>(ws, ao, q0, q1, src, gs, lane, acc);
+  else oloop_any<2, 1, MOE_CPOL_NT>(ws, ao, q0, q1, src, gs, lane, acc);
   const int n = lane & 31, gb = lane >> 5;
 #pragma unroll
   for (int i = 0; i < 2; i++)
@@ -860,7 +862,9 @@ void k_down_ol(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   const wstream ws[1] = {make_wstream32(w_d, (size_t)it.x * tiles + 2 * t32, NQ4)};
   const aoff32 ao = make_aoff32(lane, NQ4);
   oring_l<1, 1, NG> r;
-  oprime_l<1, 1, NG, 0>(r, ws, ao, NQ);
+  const bool split = (it.w & MOE_ITEM_SPLIT) != 0;  // else non-temporal weights: no other item reads them
+  if (split) oprime_l<1, 1, NG, 0>(r, ws, ao, NQ);
+  else oprime_l<1, 1, NG, MOE_CPOL_NT>(r, ws, ao, NQ);
   u32x4_t *bl = reinterpret_cast<u32x4_t *>(lds);
   float *dl = reinterpret_cast<float *>(lds + (KB / 2) * 64 * 4);
   stage_octet_lds(hs, hd, row0, nt, KB, bl, dl, threadIdx.x, 256);
@@ -871,7 +875,11 @@ void k_down_ol(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
 #pragma unroll
   for (int e = 0; e < 16; e++) acc[0][0][e] = 0.0f;
   load_bq32_lds<1, 0, 0>(r.b[0], bl, dl, lane, dlo, 0);
-  olfixed_from<0, NQ, 1, 1, NG, 0, 0, 0>(r, ws, ao, bl, dl, lane, dlo, lane_upper32(lane), lane_bscale32(lane), acc);
+  if (split)
+    olfixed_from<0, NQ, 1, 1, NG, 0, 0, 0>(r, ws, ao, bl, dl, lane, dlo, lane_upper32(lane), lane_bscale32(lane), acc);
+  else
+    olfixed_from<0, NQ, 1, 1, NG, MOE_CPOL_NT, 0, 0>(r, ws, ao, bl, dl, lane, dlo, lane_upper32(lane),
+                                                     lane_bscale32(lane), acc);
   const bool live = t < nt;
   const int rr = row0 + (live ? t : 0);
   const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
