@@ -9,7 +9,10 @@
 // instead of running its tokens through one workgroup in turn, and the
 // items of one expert are adjacent in the grid, so their re-reads of the
 // same weight tiles are issued at about the same time (and by the same XCD:
-// a row of the grid is a multiple of 8 workgroups wide) and hit L2.
+// a row of the grid is a multiple of 8 workgroups wide) and hit L2.  Only
+// those items (MOE_ITEM_SPLIT) load their weights with the default cache
+// policy; an expert of one item is read once per call, so its tiles stream
+// non-temporal, as in decode, and leave the caches to data read again.
 //
 // B operand straight from global memory.  The activations (x: quantized
 // once per call by k_group's extra workgroups; h: written by the gate/up
