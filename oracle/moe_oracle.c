@@ -444,6 +444,91 @@ int mo_moe_forward(const mo_layer *L, int T, const float *x,
 }
 
 /* ------------------------------------------------------------------------ */
+/* exact h (parity checker: the yardstick for f32 summation-order error)    */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+  const mo_layer *L;
+  int T, P, R, nthreads, tid;
+  const int32_t *ids;
+  const int8_t *xq;
+  const uint16_t *xd;
+  double *h; /* [R][F] */
+} hx_arg;
+
+/* One row of gate or up in double: every block term isum * e8m0_half(e) *
+ * fp16(d) is exact in double (|isum| < 2^17, a power of two, an 11-bit
+ * mantissa), and the 2^-53 rounding of the sum is far below any f32 error. */
+static double dot_exact(int K, const uint8_t *wrow, const int8_t *qs, const uint16_t *d) {
+  double acc = 0.0;
+  for (int b = 0; b < K / MO_QK; b++) {
+    const uint8_t *blk = wrow + (size_t)b * MO_MXFP4_BYTES;
+    acc += (double)mo_block_isum(blk, qs + (size_t)b * MO_QK) * (double)mo_e8m0_half(blk[0]) *
+           (double)mo_fp16_to_fp32(d[b]);
+  }
+  return acc;
+}
+
+static void *hx_worker(void *argp) {
+  hx_arg *a = (hx_arg *)argp;
+  const mo_layer *L = a->L;
+  const int H = L->H, F = L->F, k = L->k, P = a->P;
+  const size_t gu_row = (size_t)(H / MO_QK) * MO_MXFP4_BYTES;
+  size_t b, e;
+  span((size_t)a->R * F, a->tid, a->nthreads, &b, &e);
+  for (size_t i = b; i < e; i++) {
+    const int r = (int)(i / (size_t)F), c = (int)(i % (size_t)F);
+    const int t = r < P ? r / k : r - P;
+    const uint8_t *gw = r < P ? L->gate[a->ids[r]] : L->sh_gate;
+    const uint8_t *uw = r < P ? L->up[a->ids[r]] : L->sh_up;
+    const int8_t *q = a->xq + (size_t)t * H;
+    const uint16_t *d = a->xd + (size_t)t * (H / MO_QK);
+    double g = dot_exact(H, gw + (size_t)c * gu_row, q, d);
+    double u = dot_exact(H, uw + (size_t)c * gu_row, q, d);
+    if (L->clamp > 1e-6f) {
+      const double l = (double)L->clamp;
+      u = u < l ? u : l;
+      u = u > -l ? u : -l;
+      g = g < l ? g : l;
+    }
+    a->h[i] = g / (1.0 + exp(-g)) * u;
+  }
+  return NULL;
+}
+
+int mo_moe_h_exact(const mo_layer *L, int T, const float *x, const int32_t *ids, double *h_routed,
+                   double *h_shared, int n_threads) {
+  if (!L || T <= 0 || !x || !ids || !h_routed) return -1;
+  if (L->H % MO_QK || L->F % MO_QK || L->k <= 0 || L->E <= 0) return -1;
+  for (int p = 0; p < T * L->k; p++)
+    if (ids[p] < 0 || ids[p] >= L->E || !L->gate[ids[p]] || !L->up[ids[p]]) return -1;
+  const int H = L->H, F = L->F, P = T * L->k;
+  const int R = P + (L->sh_gate && h_shared ? T : 0);
+  if (n_threads < 1) n_threads = 1;
+  int8_t *xq = (int8_t *)malloc((size_t)T * H);
+  uint16_t *xd = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * (H / MO_QK));
+  double *h = (double *)malloc(sizeof(double) * (size_t)R * F);
+  pthread_t *th = (pthread_t *)malloc(sizeof(pthread_t) * (size_t)n_threads);
+  hx_arg *args = (hx_arg *)malloc(sizeof(hx_arg) * (size_t)n_threads);
+  if (!xq || !xd || !h || !th || !args) {
+    free(xq); free(xd); free(h); free(th); free(args);
+    return -1;
+  }
+  for (int t = 0; t < T; t++)
+    mo_quantize_q8_0(x + (size_t)t * H, H, xq + (size_t)t * H, xd + (size_t)t * (H / MO_QK));
+  for (int i = 0; i < n_threads; i++) {
+    args[i] = (hx_arg){L, T, P, R, n_threads, i, ids, xq, xd, h};
+    if (i) pthread_create(&th[i], NULL, hx_worker, &args[i]);
+  }
+  hx_worker(&args[0]);
+  for (int i = 1; i < n_threads; i++) pthread_join(th[i], NULL);
+  memcpy(h_routed, h, sizeof(double) * (size_t)P * F);
+  if (R > P) memcpy(h_shared, h + (size_t)P * F, sizeof(double) * (size_t)T * F);
+  free(xq); free(xd); free(h); free(th); free(args);
+  return 0;
+}
+
+/* ------------------------------------------------------------------------ */
 /* synthetic weights                                                        */
 /* ------------------------------------------------------------------------ */
 

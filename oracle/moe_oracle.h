@@ -128,6 +128,15 @@ int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
 int mo_moe_forward_from_h(const mo_layer *L, int T, const int32_t *ids, const float *wts,
                           const float *h, float *out, float *per_slot, int n_threads);
 
+/* The SwiGLU output h of the same block with gate and up summed exactly (in
+ * double: each block term isum * e8m0_half(e) * fp16(d) is exact there) and
+ * clamp / SiLU / product in double, from the same Q8_0 of x as
+ * mo_moe_forward.  h_routed [T][k][F], h_shared [T][F] (NULL: not computed).
+ * No counterpart in ggml: it is the parity checker's yardstick, against
+ * which the f32 error of this oracle and of the device are both measured. */
+int mo_moe_h_exact(const mo_layer *L, int T, const float *x, const int32_t *ids,
+                   double *h_routed, double *h_shared, int n_threads);
+
 /* ---- synthetic weights ------------------------------------------------ */
 
 /* SplitMix64 finalizer (Steele, Lea, Flood 2014). */

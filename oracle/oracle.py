@@ -26,6 +26,7 @@ _i8p = ctypes.POINTER(ctypes.c_int8)
 _u16p = ctypes.POINTER(ctypes.c_uint16)
 _i32p = ctypes.POINTER(ctypes.c_int32)
 _f32p = ctypes.POINTER(ctypes.c_float)
+_f64p = ctypes.POINTER(ctypes.c_double)
 
 
 class _Layer(ctypes.Structure):
@@ -80,6 +81,9 @@ def lib():
         L.mo_moe_forward_from_h.restype = ctypes.c_int
         L.mo_moe_forward_from_h.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _i32p, _f32p, _f32p, _f32p,
                                             _f32p, ctypes.c_int]
+        L.mo_moe_h_exact.restype = ctypes.c_int
+        L.mo_moe_h_exact.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _f32p, _i32p, _f64p, _f64p,
+                                     ctypes.c_int]
         L.mo_mix64.restype = ctypes.c_uint64
         L.mo_mix64.argtypes = [ctypes.c_uint64]
         L.mo_gen_key.restype = ctypes.c_uint64
@@ -258,6 +262,24 @@ class OracleLayer:
             res["h"] = hr
             res["h_shared"] = hs
         return res
+
+    def h_exact(self, x: np.ndarray, ids: np.ndarray, n_threads: int = 1):
+        """The SwiGLU output with gate/up summed exactly in float64 (same
+        Q8_0 of x as forward): (h [T, k, F] float64, shared [T, F] or None).
+        The yardstick of the parity checker: the f32 error of forward's h and
+        of the device's h are both measured against it."""
+        x = np.ascontiguousarray(x, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        T = x.shape[0]
+        hr = np.empty((T, self.k, self.F), np.float64)
+        hs = np.empty((T, self.F), np.float64) if self.shared else None
+        s, keep = self._struct()
+        rc = lib().mo_moe_h_exact(ctypes.byref(s), T, _p(x, _f32p), _p(ids, _i32p), _p(hr, _f64p),
+                                  None if hs is None else _p(hs, _f64p), int(n_threads))
+        del keep
+        if rc != 0:
+            raise ValueError("oracle h_exact rejected its arguments")
+        return hr, hs
 
     def forward_from_h(self, ids: np.ndarray, wts: np.ndarray, h: np.ndarray, h_shared=None,
                        n_threads: int = 1, per_slot: bool = False):

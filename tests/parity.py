@@ -42,8 +42,9 @@ def assert_rms_close(got, ref, tol=TOL, what=""):
 
 
 class Taps:
-    """Stands in for the block in check_block when the h taps were already
-    read (a subset of the tokens of a larger call)."""
+    """Stands in for the block in check_block when the h taps are at hand
+    already, in the oracle's row order (routed [T, k, F], shared [T, F] or
+    None): read back from another process, or planted by a CPU test."""
 
     def __init__(self, h, h_shared):
         self.h, self.h_shared = h, h_shared
@@ -71,33 +72,110 @@ def _same_codes(oracle, a, b):
     return np.array_equal(qa, qb) and np.array_equal(da, db)
 
 
+# Stage-1 gates on h, in units of the oracle's own f32 error (both measured
+# against the exact float64 h of the same Q8_0(x), oracle.OracleLayer.h_exact).
+# On MI355X every kernel path measured at most 1.00x over a call and 1.63x in
+# a row (the clamp-active and sweep cases); sequential-order kernels sit at 1.
+H_CALL_FACTOR = 2.0   # RMS over the call's h values
+H_ROW_FACTOR = 4.0    # RMS over one h row, against the larger of its own and
+                      # the call's pooled oracle error
+# Stage-2 bound on Q8_0(h) codes that come out different on the two sides:
+# at most FLIP_FACTOR x the number expected from errors of the oracle's size,
+# plus FLIP_SLACK.
+FLIP_FACTOR = 4.0
+FLIP_SLACK = 4
+
+
+def _rms_rows(a):
+    return np.sqrt(np.mean(np.square(a), axis=-1))
+
+
+def _h_gate(dev, ora, exact, what):
+    """dev, ora: f32 h rows [N, F]; exact: float64 [N, F].  The device's error
+    must be of the size f32 summation order explains, measured by the
+    oracle's own f32 error on the same rows."""
+    dev, ora, exact = (np.asarray(a, np.float64).reshape(-1, np.shape(a)[-1]) for a in (dev, ora, exact))
+    e_dev, e_ora = dev - exact, ora - exact
+    rms_exact = float(np.sqrt(np.mean(np.square(exact))))
+    call_floor = 2.0 ** -24 * rms_exact + 1e-30  # one f32 rounding of h itself
+    e_ora_call = max(float(np.sqrt(np.mean(np.square(e_ora)))), call_floor)
+    call = float(np.sqrt(np.mean(np.square(e_dev)))) / e_ora_call
+    # A row's yardstick: its own oracle error, or the call's pooled one scaled
+    # to the row's magnitude, whichever is larger.  With a clamp engaged most
+    # values of a row are clamped, and its own error can come from one or two
+    # values (or from nothing but h's final rounding): too noisy alone.
+    pooled = e_ora_call * _rms_rows(exact) / max(rms_exact, 1e-30)
+    floor_rows = 2.0 ** -24 * _rms_rows(exact) + 1e-30
+    rows = _rms_rows(e_dev) / np.maximum(np.maximum(_rms_rows(e_ora), pooled), floor_rows)
+    say(f"{what}: rms(h err) device/oracle = {call:.3f} over the call, rows max {rows.max():.3f} "
+        f"median {float(np.median(rows)):.3f}")
+    assert call <= H_CALL_FACTOR, f"{what}: h error {call:.2f}x the oracle's own f32 error over the call"
+    assert rows.max() <= H_ROW_FACTOR, (f"{what}: h error {rows.max():.2f}x the oracle's own f32 error in row "
+                                        f"{int(np.argmax(rows))}")
+
+
+def _code_flips(oracle, dev, ora, exact):
+    """(observed, expected) code differences of Q8_0(h) between the device's
+    and the oracle's h rows.  Observed: codes that differ in blocks whose d
+    agrees, plus blocks whose d differs.  Expected, for two f32 orders with
+    errors of the oracle's size: a code flips when a rounding boundary falls
+    between the two values, with probability ~ their distance in code units
+    (1.5 x the oracle's own distance from the exact h, for the difference of
+    two such errors); a block's d (fp16 of amax/127) flips with probability ~
+    amax's relative distance over fp16's 2^-11 step."""
+    F = np.shape(dev)[-1]
+    dev = np.ascontiguousarray(dev, np.float32).reshape(-1, F)
+    ora = np.ascontiguousarray(ora, np.float32).reshape(-1, F)
+    exact = np.asarray(exact, np.float64).reshape(-1, F)
+    qa, da = oracle.quantize_q8_0(dev)
+    qb, db = oracle.quantize_q8_0(ora)
+    same_d = (da == db)[..., None]
+    observed = int(((qa != qb).reshape(da.shape + (32,)) & same_d).sum() + (~same_d).sum())
+    amax = np.abs(ora.reshape(da.shape + (32,))).max(axis=-1).astype(np.float64)
+    step = 127.0 / np.maximum(amax, 1e-30)
+    dist = np.abs(ora.astype(np.float64) - exact).reshape(da.shape + (32,))
+    p_code = np.minimum(1.0, 1.5 * dist * step[..., None]).sum()
+    a64 = np.abs(exact.reshape(da.shape + (32,))).max(axis=-1)
+    p_d = np.minimum(1.0, 1.5 * np.abs(amax - a64) / np.maximum(amax, 1e-30) / 2.0 ** -11).sum()
+    return observed, float(p_code + p_d)
+
+
 def check_block(oracle, L, blk, shape, x, ids, wts, got, what, n_threads=16, per_slot=False, tol=TOL):
     """Parity of one forward, in two stages.
 
-    1. gate/up + clamp + SwiGLU: the GPU's h against the oracle's h, max|dh|
-       <= 2e-4 * max|h| per row (only the f32 summation order differs; the
-       bound leaves room for cancellation in the gate/up sums, which is
-       large when the clamp is active).
+    1. gate/up + clamp + SwiGLU: the GPU's h and the oracle's (f32) h are
+       both measured against the exact float64 h of the same Q8_0(x)
+       (OracleLayer.h_exact).  The GPU's error may be at most H_CALL_FACTOR
+       times the oracle's own f32 error in RMS over the call, and
+       H_ROW_FACTOR times it in any one h row: only the f32 summation order
+       may differ, so any error beyond that scale (a dropped or misscaled
+       block term, a wrong clamp) fails here.
     2. The output, max|d| <= tol * RMS: against the oracle run end to end
        for every token (per_slot: every (token, slot) row) whose Q8_0(h)
        codes come out identical on both sides; where an h value sits so
        close to a Q8_0 rounding boundary that the two f32 orders round it to
        neighbouring codes, against the oracle's down path fed the GPU's h
        (the same Q8_0(h) codes: the activation quantization reproduced).
-       The number of such tokens (rows) is reported.
+       The number of such code differences is bounded by what errors of
+       the oracle's size explain (FLIP_FACTOR x expected + FLIP_SLACK).
 
     got: [T, H], or [T, k, H] with per_slot (the weighted per-slot rows, the
     shared expert not included)."""
     ref = L.forward(x, ids, wts, n_threads=n_threads, taps=True, per_slot=per_slot)
+    h64, h64s = L.h_exact(x, ids, n_threads=n_threads)
     hg, hgs = gpu_h(blk, oracle, shape, ids, shared=False if per_slot else None)
-    pairs = [(hg, ref["h"], "h")] + ([(hgs, ref["h_shared"], "h shared")] if hgs is not None else [])
-    for a, b, nm in pairs:
-        a2 = a.reshape(-1, a.shape[-1]).astype(np.float64)
-        b2 = b.reshape(-1, b.shape[-1]).astype(np.float64)
-        scale = np.maximum(np.abs(b2).max(axis=1, keepdims=True), 1e-30)
-        worst = float((np.abs(a2 - b2) / scale).max())
-        say(f"{what} {nm}: max|dh|/max|h| = {worst:.3e}")
-        assert worst <= 2e-4, f"{what} {nm}: max|dh|/max|h| = {worst:.3e}"
+    F = hg.shape[-1]
+    parts = [(hg, ref["h"], h64)] + ([(hgs, ref["h_shared"], h64s)] if hgs is not None else [])
+    _h_gate(np.concatenate([p[0].reshape(-1, F) for p in parts]),
+            np.concatenate([p[1].reshape(-1, F) for p in parts]),
+            np.concatenate([p[2].reshape(-1, F) for p in parts]), f"{what} h")
+    observed, expected = 0, 0.0
+    for a, b, c in parts:
+        o_, e_ = _code_flips(oracle, a, b, c)
+        observed, expected = observed + o_, expected + e_
+    say(f"{what}: {observed} Q8_0(h) code differences, {expected:.2f} expected from f32 order")
+    assert observed <= FLIP_FACTOR * expected + FLIP_SLACK, (
+        f"{what}: {observed} Q8_0(h) code differences, more than f32 summation order explains ({expected:.2f})")
     T, k = ids.shape
     flips = []
     for t in range(T):
@@ -126,6 +204,7 @@ def check_block(oracle, L, blk, shape, x, ids, wts, got, what, n_threads=16, per
     unit = "rows" if per_slot else "tokens"
     total = T * k if per_slot else T
     say(f"{what}: {len(flips)} of {total} {unit} with an h value on a Q8_0 rounding boundary", flips[:16])
+    assert len(flips) <= observed
     return ref
 
 

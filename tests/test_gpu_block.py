@@ -12,7 +12,7 @@ import pytest
 
 import moe_block as mb
 import workloads as wl
-from parity import Taps, assert_rms_close, check_block, gpu_h, oracle_layer, run_block, say
+from parity import assert_rms_close, check_block, oracle_layer, run_block, say
 
 pytestmark = pytest.mark.gpu
 
@@ -268,21 +268,16 @@ def test_c3_small_batch_zipf(blk, torch_dev, oracle, v3, T):
 @pytest.mark.parametrize("zipf", [True, False])
 def test_c4_prefill_chunk(blk, torch_dev, oracle, v3, zipf):
     """T=512: the whole chunk runs on the GPU (hot experts split over many
-    work items); the oracle checks every 8th token plus every token routed to
-    the hottest expert (each token's output depends on its own row only)."""
+    work items) and the oracle checks every token: h of every (token, slot)
+    and shared row, and every token's output."""
     T = 512
     x, lg = wl.make_inputs(v3, T, 90 + int(zipf), zipf=zipf)
     ids, wts = oracle.route(lg, 8, v3.route_mode, norm=True)
     g = oracle.group(ids, v3.n_expert)
-    hot = int(np.argmax(g["counts"]))
-    sub = sorted(set(range(0, T, 8)) | set(np.nonzero((ids == hot).any(axis=1))[0][:24].tolist()))
-    say("C4 T=512 zipf", zipf, "distinct", g["distinct"], "hottest", hot, int(g["counts"].max()), "checked", len(sub))
+    say("C4 T=512 zipf", zipf, "distinct", g["distinct"], "hottest", int(np.argmax(g["counts"])),
+        int(g["counts"].max()))
     got = run_block(blk, torch_dev, 2, x, ids, wts)
-    hg, hgs = gpu_h(blk, oracle, v3, ids)
-    L = oracle_layer(oracle, v3, 202, 2, ids[sub])
-    # the subset's h rows, as the check's GPU taps
-    blk_sub = Taps(hg[sub], hgs[sub])
-    check_block(oracle, L, blk_sub, v3, x[sub], ids[sub], wts[sub], got[sub], "C4")
+    check_block(oracle, oracle_layer(oracle, v3, 202, 2, ids), blk, v3, x, ids, wts, got, "C4")
 
 
 @pytest.mark.parametrize("T", [16, 64])

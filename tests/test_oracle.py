@@ -230,6 +230,37 @@ def test_forward_vs_float64(oracle, shared, clamp):
         assert np.abs(h).max() > 0
 
 
+@pytest.mark.parametrize("shared,clamp", [(False, 0.0), (True, 0.0), (True, 0.75)])
+def test_h_exact_vs_float64(oracle, shared, clamp):
+    """The parity checker's yardstick: h with gate/up summed in float64 equals
+    the numpy float64 restatement (dequantized matrices times the dequantized
+    Q8_0 of x) to float64 rounding, routed and shared rows alike, with the
+    clamp engaged (large exponents) or not; and the oracle's own f32 h sits
+    within f32 summation error of it."""
+    H, F, E, k, T = 256, 96, 6, 3, 4
+    L = _tiny_layer(oracle, 41, H, F, E, k, shared, clamp, e_lo=128 if clamp else 120, e_span=4)
+    rng = np.random.default_rng(42)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    wts = np.ones((T, k), np.float32)
+    h, hs = L.h_exact(x, ids, n_threads=3)
+    _, want = np_ref.moe_forward_f64(L, x, ids, wts, oracle.quantize_q8_0)
+    scale = np.abs(want).max()
+    assert np.max(np.abs(h - want)) <= 1e-13 * scale
+    if clamp:
+        assert np.abs(want).max() <= clamp * clamp  # silu(g) <= g <= L and |u| <= L
+    if shared:
+        xq, xd = oracle.quantize_q8_0(x)
+        xa = np_ref.q8_dequant(xq, xd)
+        G, U = (np_ref.dequant_blocks(m) for m in L.shared[:2])
+        want_s = np_ref.swiglu(xa @ G.T, xa @ U.T, clamp)
+        assert np.max(np.abs(hs - want_s)) <= 1e-13 * np.abs(want_s).max()
+    else:
+        assert hs is None
+    f32 = L.forward(x, ids, wts, taps=True)["h"]
+    assert 0 < np.max(np.abs(f32 - h)) <= 1e-5 * scale
+
+
 def test_forward_clamp_engages(oracle):
     # large weights make |g|, |u| far exceed a small limit: output must differ from unclamped
     H, F, E, k, T = 64, 64, 4, 2, 2
