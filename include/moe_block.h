@@ -91,6 +91,14 @@ const char *moe_ctx_last_error(const moe_ctx *ctx);
 const char *moe_status_str(moe_status s);
 uint64_t moe_ctx_budget_left(const moe_ctx *ctx);
 
+/* Free and total device memory of `device` (hipMemGetInfo), without a
+ * context: what a residency planner reads before choosing a budget.  The
+ * reference's placement reads the same two numbers per device and holds
+ * MOESERV_RESERVE_MB of the free memory back (ggml_backend_dev_memory in
+ * moe_place_probe, moe-serv/src/moe_place.h:56-78).  MOE_ERR_NO_DEVICE
+ * when the device does not exist. */
+moe_status moe_device_memory(int device, uint64_t *free_bytes, uint64_t *total_bytes);
+
 /* Pre-size the per-call scratch for up to max_tokens tokens per call on
  * layers of this shape, so that later moe_forward / graph capture calls do
  * no allocation (moe_tp_set_dims, moe_tp.h:494-545, fixes its scratch the

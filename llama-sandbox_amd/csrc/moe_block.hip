@@ -457,6 +457,22 @@ extern "C" const char *moe_status_str(moe_status s) {
   return "unknown status";
 }
 
+extern "C" moe_status moe_device_memory(int device, uint64_t *free_bytes, uint64_t *total_bytes) {
+  if (!free_bytes || !total_bytes) return MOE_ERR_INVALID_ARG;
+  *free_bytes = *total_bytes = 0;
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return MOE_ERR_NO_DEVICE;
+  int prev = 0;
+  if (hipGetDevice(&prev) != hipSuccess || hipSetDevice(device) != hipSuccess) return MOE_ERR_NO_DEVICE;
+  size_t fr = 0, tot = 0;
+  const hipError_t e = hipMemGetInfo(&fr, &tot);
+  (void)hipSetDevice(prev);
+  if (e != hipSuccess) return MOE_ERR_HIP;
+  *free_bytes = fr;
+  *total_bytes = tot;
+  return MOE_OK;
+}
+
 extern "C" uint64_t moe_ctx_budget_left(const moe_ctx *c) {
   return c && c->budget > c->used ? c->budget - c->used : 0;
 }

@@ -21,10 +21,14 @@
 // Environment (the reference's names, so that a drop-in keeps its scripts):
 //   MOESERV_DISABLE        claim nothing (moe_node_claimed)
 //   MOESERV_TP_BUDGET_MB   device bytes the expert layers may use (MB; 0 =
-//                          every layer stays on the CPU); default: no cap
+//                          every layer stays on the CPU); default: the
+//                          device's free memory less MOESERV_RESERVE_MB
+//   MOESERV_RESERVE_MB     device memory held back from the expert layers
+//                          for the per-call scratch (default 1024)
 //   MOESERV_PROFILE=<p>    per-split phase rows written to <p>-<pid>.csv at
-//                          teardown, one row per split (dev 0 = the GPU,
-//                          -1 = the CPU delegate)
+//                          teardown, one row per split in the reference's 14
+//                          columns (dev 0 = the GPU, -1 = the CPU delegate),
+//                          and the per-device means on stderr
 #include "ggml-backend-impl.h"
 #include "ggml.h"
 #include "moe_block.h"
@@ -49,12 +53,17 @@ namespace {
 // process-wide state (the backend is one set of singletons, driven by the
 // scheduler thread one split at a time, as the reference's is)
 
+// One MOESERV_PROFILE row, in the reference's columns (moe-serv/src/moe_prof.h:36-56).
+// A device split is one pass over all its tokens, so chunk = n_tok and n_chunks = 1;
+// build = graph_compute's own work before the device call (node conversion and the
+// split parse); alloc = making the layer resident, on its first split only (the
+// per-call scratch is reused, so there is no per-call allocation to time); free is 0.
 struct split_row {
   uint64_t call;
   int dev;  // 0: the GPU, -1: the CPU delegate
   int n_nodes;
-  int64_t n_tok, n_exp;
-  double upload_us, compute_us, read_us, total_us;
+  int64_t n_tok, chunk, n_chunks, n_exp;
+  double build_us, alloc_us, upload_us, compute_us, read_us, free_us, total_us;
 };
 
 struct backend_state {
@@ -148,7 +157,9 @@ struct node_map {
 ggml_backend_t cpu_backend() {
   if (!g_state.cpu) {
     g_state.cpu = ggml_backend_init_by_type(GGML_BACKEND_DEVICE_TYPE_CPU, nullptr);
-    if (!g_state.cpu) fprintf(stderr, "%s: no CPU backend in the registry to delegate to\n", MOE_GGML_NAME);
+    if (!g_state.cpu)
+      fprintf(stderr, "%s: the host registry holds no CPU backend, so a split the device declines cannot run\n",
+              MOE_GGML_NAME);
   }
   return g_state.cpu;
 }
@@ -161,13 +172,29 @@ bool profiling() {
   return !g_state.profile_prefix.empty();
 }
 
+// The residency budget: MOESERV_TP_BUDGET_MB when set; otherwise the device's
+// free memory less MOESERV_RESERVE_MB (default 1 GiB), held back for the
+// per-call scratch so that a later, larger call (a prefill after decode) still
+// finds room (the reference's placement holds the same reserve per device,
+// moe-serv/src/moe_place.h:56-78).
+uint64_t residency_budget() {
+  if (const char *b = getenv("MOESERV_TP_BUDGET_MB")) return (uint64_t)strtoull(b, nullptr, 10) << 20;
+  uint64_t reserve = 1024ull << 20;
+  if (const char *r = getenv("MOESERV_RESERVE_MB")) reserve = (uint64_t)strtoull(r, nullptr, 10) << 20;
+  uint64_t free_b = 0, total_b = 0;
+  if (moe_device_memory(0, &free_b, &total_b) != MOE_OK) return UINT64_MAX;  // ctx creation reports it
+  const uint64_t budget = free_b > reserve ? free_b - reserve : 0;
+  fprintf(stderr, "%s-gfx950: residency budget %llu MB (%llu MB free, %llu MB held back)\n", MOE_GGML_NAME,
+          (unsigned long long)(budget >> 20), (unsigned long long)(free_b >> 20), (unsigned long long)(reserve >> 20));
+  return budget;
+}
+
 // Device context on first use: absent device, NO_DEVICE or a zero budget all
 // leave ctx null and every split on the CPU.
 moe_ctx *device_ctx() {
   if (!g_state.ctx_tried) {
     g_state.ctx_tried = true;
-    uint64_t budget = UINT64_MAX;
-    if (const char *b = getenv("MOESERV_TP_BUDGET_MB")) budget = (uint64_t)strtoull(b, nullptr, 10) << 20;
+    const uint64_t budget = residency_budget();
     const moe_status st = moe_ctx_create(0, budget, &g_state.ctx);
     if (st != MOE_OK) {
       fprintf(stderr, "%s-gfx950: no device context (%s); every split runs on the CPU\n", MOE_GGML_NAME,
@@ -178,6 +205,44 @@ moe_ctx *device_ctx() {
     }
   }
   return g_state.ctx;
+}
+
+long long us(double v) { return (long long)llround(v); }
+
+// <prefix>-<pid>.csv in the reference's columns (integer microseconds), then the
+// per-device means on stderr (moe-serv/src/moe_prof.h:94-137).
+void write_profile() {
+  char path[1024];
+  snprintf(path, sizeof path, "%s-%d.csv", g_state.profile_prefix.c_str(), (int)getpid());
+  FILE *f = fopen(path, "wb");
+  if (!f) {
+    fprintf(stderr, "%s-gfx950: cannot write %s\n", MOE_GGML_NAME, path);
+    return;
+  }
+  fprintf(f, "call,dev,n_nodes,n_tok,chunk,n_chunks,n_exp_loads,"
+             "build_us,alloc_us,upload_us,compute_us,read_us,free_us,total_us\n");
+  for (const split_row &r : g_state.rows)
+    fprintf(f, "%llu,%d,%d,%lld,%lld,%lld,%lld,%lld,%lld,%lld,%lld,%lld,%lld,%lld\n", (unsigned long long)r.call,
+            r.dev, r.n_nodes, (long long)r.n_tok, (long long)r.chunk, (long long)r.n_chunks, (long long)r.n_exp,
+            us(r.build_us), us(r.alloc_us), us(r.upload_us), us(r.compute_us), us(r.read_us), us(r.free_us),
+            us(r.total_us));
+  fclose(f);
+  fprintf(stderr, "%s-gfx950: profile -> %s (%zu rows)\n", MOE_GGML_NAME, path, g_state.rows.size());
+  for (int dev = -1; dev <= 0; dev++) {
+    double n = 0, sum[7] = {0, 0, 0, 0, 0, 0, 0};
+    for (const split_row &r : g_state.rows) {
+      if (r.dev != dev) continue;
+      n++;
+      const double v[7] = {r.build_us, r.alloc_us, r.upload_us, r.compute_us, r.read_us, r.free_us, r.total_us};
+      for (int i = 0; i < 7; i++) sum[i] += v[i];
+    }
+    if (n == 0) continue;
+    fprintf(stderr,
+            "%s-gfx950:   %-8s n=%-6lld mean us: build %.1f alloc %.1f upload %.1f compute %.1f read %.1f free %.1f"
+            " | total %.1f\n",
+            MOE_GGML_NAME, dev < 0 ? "cpu" : "gfx950", (long long)n, sum[0] / n, sum[1] / n, sum[2] / n, sum[3] / n,
+            sum[4] / n, sum[5] / n, sum[6] / n);
+  }
 }
 
 void report_and_reset() {
@@ -193,20 +258,7 @@ void report_and_reset() {
               (double)cs.expert_loads / (double)cs.calls);
     }
   }
-  if (profiling() && !g_state.rows.empty()) {
-    char path[1024];
-    snprintf(path, sizeof path, "%s-%d.csv", g_state.profile_prefix.c_str(), (int)getpid());
-    if (FILE *f = fopen(path, "wb")) {
-      fprintf(f, "call,dev,n_nodes,n_tok,n_exp_loads,upload_us,compute_us,read_us,total_us\n");
-      for (const split_row &r : g_state.rows)
-        fprintf(f, "%llu,%d,%d,%lld,%lld,%.1f,%.1f,%.1f,%.1f\n", (unsigned long long)r.call, r.dev, r.n_nodes,
-                (long long)r.n_tok, (long long)r.n_exp, r.upload_us, r.compute_us, r.read_us, r.total_us);
-      fclose(f);
-      fprintf(stderr, "%s-gfx950: profile -> %s (%zu rows)\n", MOE_GGML_NAME, path, g_state.rows.size());
-    } else {
-      fprintf(stderr, "%s-gfx950: cannot write %s\n", MOE_GGML_NAME, path);
-    }
-  }
+  if (profiling() && !g_state.rows.empty()) write_profile();
   if (g_state.ctx) moe_ctx_destroy(g_state.ctx);
   ggml_backend_t cpu = g_state.cpu;
   g_state = backend_state();
@@ -396,13 +448,28 @@ const char *backend_get_name(ggml_backend_t backend) {
 
 void backend_free(ggml_backend_t backend) { delete backend; }
 
+// The n_tok of a split that did not parse: the first MUL_MAT_ID's ids tensor,
+// as the reference counts its CPU rows (moe_backend.cpp:469-480).
+int64_t tokens_of(ggml_cgraph *cgraph) {
+  for (int i = 0; i < ggml_graph_n_nodes(cgraph); i++) {
+    const ggml_tensor *t = ggml_graph_node(cgraph, i);
+    if (t->op == GGML_OP_MUL_MAT_ID && t->src[2]) return t->src[2]->ne[1];
+  }
+  return 0;
+}
+
 enum ggml_status run_on_cpu(ggml_cgraph *cgraph, split_row &row, double t0) {
   g_state.n_cpu++;
   ggml_backend_t cpu = cpu_backend();
   if (!cpu) return GGML_STATUS_FAILED;
+  const double tc = now_us();
   const enum ggml_status st = ggml_backend_graph_compute(cpu, cgraph);
   if (profiling()) {
     row.dev = -1;
+    if (!row.n_tok) row.n_tok = tokens_of(cgraph);
+    row.chunk = row.n_tok;
+    row.n_chunks = 1;
+    row.compute_us = now_us() - tc;
     row.total_us = now_us() - t0;
     g_state.rows.push_back(row);
   }
@@ -454,7 +521,9 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
   for (int i = 0; i < n; i++) nodes[i] = m.get(ggml_graph_node(cgraph, i), 6);
   moe_split sp;
   char why[256];
-  if (moe_split_parse(nodes.data(), n, &sp, why, sizeof why) != MOE_OK) {
+  const bool parsed = moe_split_parse(nodes.data(), n, &sp, why, sizeof why) == MOE_OK;
+  row.build_us = now_us() - t0;
+  if (!parsed) {
     refusal(why);
     return run_on_cpu(cgraph, row, t0);
   }
@@ -479,8 +548,10 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
       refusal(why);
     } else {
       d.clamp = L;
+      const double ta = now_us();
       const moe_status st = moe_layer_upload(ctx, sp.layer, &d, sp.gate_w->data, sp.up_w->data, sp.down_w->data,
                                              nullptr, nullptr, nullptr);
+      row.alloc_us = now_us() - ta;
       ok = st == MOE_OK;
       if (ok) {
         uint64_t bytes = 0;
@@ -506,6 +577,8 @@ enum ggml_status backend_graph_compute(ggml_backend_t backend, ggml_cgraph *cgra
     moe_call_stats cs;
     if (moe_call_stats_read(ctx, &cs, 0) == MOE_OK) {
       row.dev = 0;
+      row.chunk = row.n_tok;
+      row.n_chunks = 1;
       row.n_exp = cs.last_experts;
       row.upload_us = cs.last_upload_us;
       row.compute_us = cs.last_compute_us;

@@ -36,6 +36,7 @@ T_GATE, T_UP, T_DOWN = 0, 1, 2
 # every entry point include/moe_block.h declares
 EXPORTS = (
     "moe_ctx_create", "moe_ctx_destroy", "moe_ctx_last_error", "moe_status_str", "moe_ctx_budget_left",
+    "moe_device_memory",
     "moe_ctx_reserve", "moe_layer_upload", "moe_layer_generate", "moe_layer_read_blocks",
     "moe_layer_release", "moe_layer_bytes", "moe_route", "moe_group", "moe_forward", "moe_forward_noalloc",
     "moe_forward_host",
