@@ -56,7 +56,8 @@ def parse():
                     help="only read a rocprofv3 kernel_trace.csv of a --workload c5 run and print the idle time "
                          "between the graph replays' kernels per layer (the launch overhead), then exit")
     ap.add_argument("--eager", action="store_true", help="time eager launches instead of the hipGraph")
-    ap.add_argument("--workload", default="c2", choices=["c1", "c2", "c3", "c4", "c5", "boundary", "server"],
+    ap.add_argument("--workload", default="c2",
+                    choices=["c1", "c2", "c3", "c4", "c5", "v4p", "f1536", "boundary", "server"],
                     help="c2 (default): the headline V3 decode line; c1/c3/c4/c5: one line per measured case of "
                          "that configuration (C1 decode, C3 T=4/16/64 Zipf, C4 T=512 uniform and Zipf, C5 40-layer "
                          "graph); boundary: V3 decode calls through the host-buffer split interface; server: "
@@ -267,7 +268,7 @@ def bench_config(args):
 
     NL = args.layers if args.layers != 8 or name != "C1" else 4
     steps, W = args.steps, args.warmup
-    if name == "C4" and steps == 256:
+    if name in ("C4", "V4P", "F1536") and steps == 256:
         steps, W = 16, 4  # defaults sized for T=512
     elif name == "C3" and steps == 256:
         steps, W = 64, 8

@@ -406,8 +406,10 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
       return MOE_ERR_NO_DEVICE;
     }
   // and the stacked-digit kernels (two 17 KiB chunk buffers, 34 KiB; set for uniformity)
-  const void *sk_kernels[] = {(const void *)k_gate_up_sk<56>, (const void *)k_gate_up_sk<32>,
-                              (const void *)k_gate_up_sk<16>, (const void *)k_down_sk<16>, (const void *)k_down_sk<8>};
+  const void *sk_kernels[] = {(const void *)k_gate_up_sk<56>, (const void *)k_gate_up_sk<48>,
+                              (const void *)k_gate_up_sk<32>, (const void *)k_gate_up_sk<16>,
+                              (const void *)k_down_sk<24>, (const void *)k_down_sk<16>, (const void *)k_down_sk<12>,
+                              (const void *)k_down_sk<8>};
   for (const void *kf : sk_kernels)
     if (hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, MOE_SK_LDS_BYTES) != hipSuccess) {
       delete c;
@@ -882,14 +884,15 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
   // where the shape has an instance and the batch averages 2 pairs per
   // expert or more, gate/up and down run on a second item list with B staged
   // in LDS: items of up to 32 rows on the stacked-digit kernels
-  // (k_gate_up_sk / k_down_sk, F = 128 * {16, 8}), else items of up to 16 rows
-  // on the octet kernels (k_gate_up_ol / k_down_ol2); below 2 pairs per
-  // expert most items hold one octet and the 8-row list with B from global
-  // memory is used
+  // (k_gate_up_sk, H = 128 * {16, 32, 48, 56}; k_down_sk, F = 128 * {8, 12,
+  // 16, 24}), else items of up to 16 rows on the octet kernels (k_gate_up_ol /
+  // k_down_ol2, H = 128 * {16, 32, 56}); below 2 pairs per expert most items
+  // hold one octet and the 8-row list with B from global memory is used
   int32_t *items16 = items + group_list_words(T, k, E);
-  const bool o2 = oct && P >= 2 * E && (F / MOE_UNIT) % 4 == 0 &&
-                  (H == 128 * 56 || H == 128 * 32 || H == 128 * 16);
-  const bool sk = o2 && (F == 128 * 16 || F == 128 * 8);
+  const bool dense = oct && P >= 2 * E && (F / MOE_UNIT) % 4 == 0;
+  const bool sk = dense && (H == 128 * 56 || H == 128 * 48 || H == 128 * 32 || H == 128 * 16) &&
+                  (F == 128 * 8 || F == 128 * 12 || F == 128 * 16 || F == 128 * 24) && H % 256 == 0;
+  const bool o2 = sk || (dense && (H == 128 * 56 || H == 128 * 32 || H == 128 * 16));
   const int BT2 = sk ? 32 : 16;
   float *htap = c->taps ? s.htap : nullptr;
   const int n_xblocks = T * (H / MOE_QK);
@@ -906,6 +909,7 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
 #define MOE_GU_ARGS16 L.m[T_GATE].w, L.m[T_UP].w, s.xq, s.xd, items16, perm, k, T, F, H, d.clamp, s.hq, s.hd, htap
     const dim3 g16(F / (4 * MOE_UNIT), group_item_cap(T, k, E, BT2));  // 4 units of F per workgroup
     if (sk && H == 128 * 56) hipLaunchKernelGGL(k_gate_up_sk<56>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
+    else if (sk && H == 128 * 48) hipLaunchKernelGGL(k_gate_up_sk<48>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
     else if (sk && H == 128 * 32) hipLaunchKernelGGL(k_gate_up_sk<32>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
     else if (sk && H == 128 * 16) hipLaunchKernelGGL(k_gate_up_sk<16>, g16, dim3(512), MOE_SK_LDS_BYTES, st, MOE_GU_ARGS16);
     else if (o2 && H == 128 * 56) hipLaunchKernelGGL(HIP_KERNEL_NAME(k_gate_up_ol<56, 4>), g16, dim3(512), 0, st, MOE_GU_ARGS16);
@@ -925,12 +929,14 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     const size_t lo = octet_lds_bytes(F / MOE_QK), lo2 = 2 * octet_lds_bytes_z(F / MOE_QK);
     // two octets per wave on the 16-row items where that list exists and two
     // workgroups' LDS (2 x 2 staged octets) fit a CU (F = 768; the stacked
-    // kernels take F = 1024 and 2048)
+    // kernels take F = 1024, 1536, 2048 and 3072)
     const dim3 gdo2(H / (32 * MOE_DOL2_WAVES), group_item_cap(T, k, E, BT2));
-    const bool dn2 = o2 && H % (32 * MOE_DOL2_WAVES) == 0;
+    const bool dn2 = o2 && !sk && H % (32 * MOE_DOL2_WAVES) == 0;
     const dim3 b2(64 * MOE_DOL2_WAVES);
 #define MOE_DN_ARGS16 L.m[T_DOWN].w, s.hq, s.hd, P + T, items16, perm, wts, F, H, s.y
     if (sk && F == 128 * 16) hipLaunchKernelGGL(k_down_sk<16>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (sk && F == 128 * 24) hipLaunchKernelGGL(k_down_sk<24>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (sk && F == 128 * 12) hipLaunchKernelGGL(k_down_sk<12>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
     else if (sk && F == 128 * 8) hipLaunchKernelGGL(k_down_sk<8>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
     else if (dn2 && F == 128 * 6) hipLaunchKernelGGL(k_down_ol2<6>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (oct && F == 128 * 16) hipLaunchKernelGGL(k_down_ol<16>, gdo, dim3(256), lo, st, MOE_DN_ARGS);

@@ -69,12 +69,23 @@ C1 = LayerShape(hidden=2048, ffn=768, n_expert=32, n_used=4, has_shared=False,
 V3 = LayerShape(hidden=7168, ffn=2048, n_expert=256, n_used=8, has_shared=True,
                 route_mode=ROUTE_SIGMOID, bf16_act=True)
 
+# Shapes beyond the configurations, for the prefill kernels' other instances:
+# the reference's DeepSeek-V4-Pro layer (hip-moe/README.md:280-286: 7168 -> 3072,
+# 384 experts, top-6 sqrt(softplus) routing renormalised and scaled by 2.5,
+# clamped SwiGLU, one shared expert), and the V3 layer with 1536-wide experts.
+V4P = LayerShape(hidden=7168, ffn=3072, n_expert=384, n_used=6, has_shared=True,
+                 route_mode=ROUTE_SQRT_SOFTPLUS, scale=2.5, clamp=10.0, bf16_act=True)
+V3F1536 = LayerShape(hidden=7168, ffn=1536, n_expert=256, n_used=8, has_shared=True,
+                     route_mode=ROUTE_SIGMOID, bf16_act=True)
+
 CONFIGS = {
     "C1": dict(shape=C1, tokens=(1,), zipf=False),
     "C2": dict(shape=V3, tokens=(1,), zipf=False),
     "C3": dict(shape=V3, tokens=(4, 16, 64), zipf=True),
     "C4": dict(shape=V3, tokens=(512,), zipf=None),  # uniform and Zipf
     "C5": dict(shape=V3, tokens=(1,), zipf=False, layers=40),
+    "V4P": dict(shape=V4P, tokens=(512,), zipf=None),
+    "F1536": dict(shape=V3F1536, tokens=(512,), zipf=None),
 }
 
 

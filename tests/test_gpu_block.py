@@ -337,16 +337,16 @@ def test_graph_replay_matches_eager(blk, torch_dev, oracle, v3, c1):
 # several H / F; pairs (T <= 4); octets with k_gate_up_o and with k_gate_up_ol (P >= 2E,
 # H = 128 * {16, 32, 56}, F without a stacked instance); down on 16-row items with one
 # and two octets (k_down_ol2<6>), k_down_ol<8, 28> and k_down_o (F / 128 without an
-# instance); the stacked-digit kernels (P >= 2E, F = 128 * {8, 16}: k_gate_up_sk<16, 32>,
-# k_down_sk<8, 16>, with experts of more than 32 rows; <56> / <16> run in the C3 T=64 and
-# C4 tests); shared expert and clamp on and off.
+# instance); the stacked-digit kernels (P >= 2E, H = 128 * {16, 32, 48, 56}, F = 128 * {8,
+# 12, 16, 24}: k_gate_up_sk<16, 32, 48, 56>, k_down_sk<8, 12, 16, 24>, with experts of
+# more than 32 rows); shared expert and clamp on and off.
 SWEEP = [
     (3072, 768, 32, 4, 1, False, 0.0, wl.ROUTE_SOFTMAX),      # decode, narrow: k_gate_up<1>
     (2048, 2048, 64, 8, 1, True, 0.0, wl.ROUTE_SIGMOID),      # decode, 256 workgroups: bal2
     (1024, 2048, 16, 5, 1, False, 4.0, wl.ROUTE_SIGMOID),     # decode, 1280 tasks: k_gate_up_bal
     (1024, 3584, 8, 2, 3, False, 0.0, wl.ROUTE_SOFTMAX),      # pairs, F = 3584
     (4096, 1024, 64, 6, 32, True, 0.0, wl.ROUTE_SIGMOID),     # stacked: k_gate_up_sk<32>, k_down_sk<8>
-    (2048, 1536, 16, 2, 20, False, 6.0, wl.ROUTE_SOFTMAX),    # octets, ol<16>, k_down_o
+    (2048, 1536, 16, 2, 20, False, 6.0, wl.ROUTE_SOFTMAX),    # stacked: k_gate_up_sk<16>, k_down_sk<12>, 2-3 rows
     (1024, 1024, 256, 8, 7, True, 0.0, wl.ROUTE_SIGMOID),     # octets, k_gate_up_o, k_down_ol<8>
     (7168, 768, 16, 4, 9, False, 0.0, wl.ROUTE_SQRT_SOFTPLUS),  # ol<56>, 16-row items, k_down_ol2<6>
     (2048, 3584, 8, 2, 33, True, 8.0, wl.ROUTE_SIGMOID),      # ol<16>, k_down_ol<28>, clamp
@@ -356,7 +356,11 @@ SWEEP = [
     (7168, 768, 8, 4, 40, False, 5.0, wl.ROUTE_SOFTMAX),      # k_down_ol2<6>, 16 + 4-row items, clamp
     (2048, 2048, 16, 4, 24, True, 0.0, wl.ROUTE_SIGMOID),     # stacked: k_gate_up_sk<16>, k_down_sk<16>
     (2048, 1024, 8, 4, 80, False, 3.0, wl.ROUTE_SOFTMAX),     # stacked, experts of 32 + n rows, clamp
-    (4096, 1536, 16, 4, 32, True, 0.0, wl.ROUTE_SIGMOID),     # ol<32> (F without a stacked instance), k_down_o
+    (4096, 1280, 16, 4, 32, True, 0.0, wl.ROUTE_SIGMOID),     # ol<32> (F without a stacked instance), k_down_o
+    (7168, 3072, 16, 6, 8, True, 6.0, wl.ROUTE_SQRT_SOFTPLUS),  # stacked: k_down_sk<24> (V4-Pro F), clamp
+    (7168, 3072, 8, 6, 64, True, 0.0, wl.ROUTE_SQRT_SOFTPLUS),  # k_down_sk<24>, experts of 48 rows
+    (7168, 1536, 16, 8, 8, True, 0.0, wl.ROUTE_SIGMOID),      # stacked: k_down_sk<12>
+    (6144, 2048, 16, 8, 40, False, 0.0, wl.ROUTE_SIGMOID),    # stacked: k_gate_up_sk<48> (glm-dsa H), 20 rows
 ]
 
 
