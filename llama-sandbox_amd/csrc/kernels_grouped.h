@@ -381,6 +381,91 @@ void k_down_g(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, 
   else dn_item<1>(w_d, src, it, perm, wts, F, H, y);
 }
 
+// ---------------------------------------------------------------------------
+// Down x router weight with the slot combine, for calls of a few tokens (the
+// pairs path, T <= MOE_DF_TMAX): one workgroup of MOE_DF_WAVES waves per
+// 32 rows of H (two 16-row tiles).  Wave w takes items w, w + MOE_DF_WAVES,
+// ... (one expert's two tiles over all of F against the item's h rows, B
+// read from the grouped h rows as in k_down_g); each (token, slot) row goes
+// to LDS and the rows of a token are added in slot order, ((y0 + y1) + ...)
+// + shared, straight into out -- k_combine's sum, with no y buffer and no
+// launch of its own.  A pair whose expert id is out of range belongs to no
+// item: its row stays 0.  per_slot: out [T][k][H] = the weighted rows.
+// grid H/32, 64*MOE_DF_WAVES threads.
+#define MOE_DF_WAVES 16
+#define MOE_DF_TMAX 4
+#define MOE_DF_SMAX 17  // slots per token: k <= 16, plus the shared expert
+#define MOE_DF_ROWS (2 * MOE_TILE)
+
+template <int NP>
+__device__ __forceinline__ void df_item(const uint8_t *__restrict__ w_d, const gsrc &src, const int4 &it,
+                                        const int32_t *__restrict__ perm, const float *__restrict__ wts, int k,
+                                        int P, int F, int H, int pair, float *ys) {
+  const int NQ = F / 128, NQ4 = moe_nq4(NQ), tiles = H / MOE_TILE, KB = F / MOE_QK;
+  const int lane = threadIdx.x & 63;
+  const int row0 = it.y, nt = it.z;
+  const bool shared = (it.w & MOE_ITEM_SHARED) != 0;
+  const size_t t0 = (size_t)it.x * tiles + 2 * pair;
+  const wstream ws[2] = {make_wstream(w_d, t0, NQ4), make_wstream(w_d, t0 + 1, NQ4)};
+  gsel gs[NP];
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    const int i = 2 * p + ((lane >> 3) & 1);
+    gs[p] = make_gsel(lane, i < nt ? row0 + i : -1, KB);
+  }
+  f32x4_t acc[NP][2];
+  gloop_any<2, NP, MOE_CPOL_NT>(ws, 0, NQ, src, gs, lane, acc);  // one item per expert (T <= 4): read once
+  const int gb = lane >> 4, tp = (lane >> 3) & 1;
+#pragma unroll
+  for (int p = 0; p < NP; p++) {
+    const int t = 2 * p + tp;
+    const bool live = t < nt;
+    const int r = row0 + (live ? t : 0);
+    const int pr = live && !shared ? perm[r] : 0;
+    const float wt = (live && !shared) ? wts[pr] : 1.0f;
+    const int tok = shared ? r - P : pr / k, slot = shared ? k : pr % k;
+#pragma unroll
+    for (int i = 0; i < 2; i++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        float v = col8_sum(acc[p][i][q]);
+        if (!shared) v = __fmul_rn(v, wt);
+        if ((lane & 7) == 0 && live) ys[(tok * MOE_DF_SMAX + slot) * MOE_DF_ROWS + i * MOE_TILE + 4 * gb + q] = v;
+      }
+  }
+}
+
+template <int NPMAX>
+__global__ __launch_bounds__(64 * MOE_DF_WAVES) void k_down_few(
+    const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd, int n_rows,
+    const int32_t *__restrict__ items, const int32_t *__restrict__ perm, const float *__restrict__ wts, int T, int k,
+    int F, int H, int shared, int per_slot, float *__restrict__ out) {
+  __shared__ float ys[MOE_DF_TMAX * MOE_DF_SMAX * MOE_DF_ROWS];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), pair = blockIdx.x, P = T * k;
+  for (int i = threadIdx.x; i < T * MOE_DF_SMAX * MOE_DF_ROWS; i += blockDim.x) ys[i] = 0.0f;
+  __syncthreads();
+  const gsrc src = make_gsrc(hs, hd, n_rows, F / MOE_QK);
+  const int n_items = items[0];
+  for (int y = wave; y < n_items; y += MOE_DF_WAVES) {
+    const int4 it = item_of(items, y);
+    if (NPMAX >= 2 && it.z > 2) df_item<(NPMAX >= 2 ? 2 : 1)>(w_d, src, it, perm, wts, k, P, F, H, pair, ys);
+    else df_item<1>(w_d, src, it, perm, wts, k, P, F, H, pair, ys);
+  }
+  __syncthreads();
+  if ((int)threadIdx.x >= T * MOE_DF_ROWS) return;
+  const int t = threadIdx.x / MOE_DF_ROWS, r = threadIdx.x % MOE_DF_ROWS;
+  const float *yt = ys + t * MOE_DF_SMAX * MOE_DF_ROWS + r;
+  const size_t col = (size_t)pair * MOE_DF_ROWS + r;
+  if (per_slot) {
+    for (int s = 0; s < k; s++) out[((size_t)t * k + s) * H + col] = yt[s * MOE_DF_ROWS];
+    return;
+  }
+  float o = yt[0];
+  for (int s = 1; s < k; s++) o = __fadd_rn(o, yt[s * MOE_DF_ROWS]);
+  if (shared) o = __fadd_rn(o, yt[k * MOE_DF_ROWS]);
+  out[(size_t)t * H + col] = o;
+}
+
 // ===========================================================================
 // Token octets on v_mfma_scale_f32_32x32x64_f8f6f4 (items of up to 8 rows).
 //

@@ -880,6 +880,9 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
                 MOE_GROUP_MAX_E);
   const bool oct = use_octets(T);
   const int BT = oct ? 8 : 4;
+  // a few tokens (the pairs path): down per 16-row tile of H with the slot
+  // combine in the same launch (k_down_few)
+  const bool few = !oct && T <= MOE_DF_TMAX && k + 1 <= MOE_DF_SMAX && H % MOE_DF_ROWS == 0;
   int32_t *counts = s.grp, *offsets = counts + E, *perm = offsets + E + 1, *inv = perm + P, *items = inv + P;
   // where the shape has an instance and the batch averages 2 pairs per
   // expert or more, gate/up and down run on a second item list with B staged
@@ -944,10 +947,17 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     else if (oct && F == 128 * 8) hipLaunchKernelGGL(k_down_ol<8>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
     else if (oct && F == 128 * 28) hipLaunchKernelGGL(k_down_ol<28>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
     else if (oct) hipLaunchKernelGGL(k_down_o, gdo, dim3(256), 0, st, MOE_DN_ARGS);
+    else if (few)
+      hipLaunchKernelGGL(k_down_few<2>, dim3(H / MOE_DF_ROWS), dim3(64 * MOE_DF_WAVES), 0, st, L.m[T_DOWN].w, s.hq,
+                         s.hd, P + T, items, perm, wts, T, k, F, H, shared, per_slot ? 1 : 0, out);
     else hipLaunchKernelGGL(k_down_g<2>, dim3(ceil_div(H / (2 * MOE_TILE), MOE_DG_WAVES), cap),
                             dim3(64 * MOE_DG_WAVES), 0, st, MOE_DN_ARGS);
 #undef MOE_DN_ARGS
 #undef MOE_DN_ARGS16
+  }
+  if (few) {  // k_down_few wrote out
+    HIPC(c, hipGetLastError());
+    return MOE_OK;
   }
   {
     prof_scope pc(c, K_COMBINE, st, s.timed);

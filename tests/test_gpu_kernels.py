@@ -124,7 +124,9 @@ def test_route_matches_oracle(blk, torch_dev, oracle, mode, E, k, T, bias):
 
 # P = 8800 (T = 1100): more than 8 steps of 64 pairs per wave, past the ids
 # k_group keeps in registers
-@pytest.mark.parametrize("T,k,E,zipf", [(1, 8, 256, False), (4, 8, 256, True), (64, 8, 256, True),
+# P <= 64 takes k_group's one-wave path: P = 8, 12, 32, 64, and E = 100 (not a multiple of 64)
+@pytest.mark.parametrize("T,k,E,zipf", [(1, 8, 256, False), (4, 8, 256, True), (8, 8, 256, True), (4, 6, 100, False),
+                                        (64, 8, 256, True),
                                         (512, 8, 256, True), (512, 8, 256, False), (3, 4, 32, False),
                                         (1100, 8, 256, True), (1100, 8, 256, False)])
 def test_group_bit_exact(blk, torch_dev, oracle, T, k, E, zipf):
@@ -145,7 +147,7 @@ def test_group_bit_exact(blk, torch_dev, oracle, T, k, E, zipf):
         np.testing.assert_array_equal(t.cpu().numpy(), g[name], err_msg=name)
 
 
-@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32), (1100, 8, 256)])
+@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32), (6, 8, 100), (1100, 8, 256)])
 def test_group_drops_out_of_range_ids(blk, torch_dev, T, k, E):
     """Out-of-range ids get no grouped row (inv = -1); the valid pairs keep
     ascending pair order within each expert (checked against a stable sort)."""
