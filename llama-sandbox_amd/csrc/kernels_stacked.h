@@ -136,11 +136,15 @@ __host__ __device__ constexpr int sdma_after() {
   return n;
 }
 
-// One MFMA step (block position POS of quad QL, block st of the chunk):
-// the MFMA, the next step's digits from LDS, the scaling, the next d.
-template <int SEL>
+// One MFMA step (block position POS of quad QL, block st of the chunk),
+// software-pipelined by one step: the MFMA goes out into its own result
+// registers, then the next step's digits are read from LDS, then the
+// previous step's result is scaled by its d into acc (PREV) while this MFMA
+// runs, then the next d.  The scaled sums reach acc in block order, as
+// without the pipelining; sk_loop adds the last step's after the loop.
+template <int SEL, bool PREV>
 __device__ __forceinline__ void sk_step(const u32x4_t &a4, uint32_t sa, skb &b, const uint32_t *nbuf, int nst,
-                                        bool next, int lane, int sb, f32x16_t &acc) {
+                                        bool next, int lane, int sb, f32x16_t &acc, f32x16_t &rp, float &dp) {
   const i32x8_t a = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
   const i32x8_t bv = {(int)b.lo.x, (int)b.lo.y, (int)b.lo.z, (int)b.lo.w,
                       (int)b.hi.x, (int)b.hi.y, (int)b.hi.z, (int)b.hi.w};
@@ -152,9 +156,13 @@ __device__ __forceinline__ void sk_step(const u32x4_t &a4, uint32_t sa, skb &b, 
   __builtin_amdgcn_sched_barrier(0);
   if (next) load_skb_v(b, nbuf, lane, nst);
   __builtin_amdgcn_sched_barrier(0);
-  acc = acc + d * r;
-  asm volatile("" : "+v"(acc));
+  if constexpr (PREV) {
+    acc = acc + dp * rp;
+    asm volatile("" : "+v"(acc));
+  }
   __builtin_amdgcn_sched_barrier(0);
+  rp = r;
+  dp = d;
   if (next) load_skb_d(b, nbuf, lane, nst);
 }
 
@@ -162,7 +170,7 @@ __device__ __forceinline__ void sk_step(const u32x4_t &a4, uint32_t sa, skb &b, 
 template <int QL, int NQ, int CPOL>
 __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1], const aoff32 &ao,
                                         const gsrc &src, const sdma &g, uint32_t *lds, int wave, int lane, int sb,
-                                        f32x16_t &acc) {
+                                        f32x16_t &acc, f32x16_t &rp, float &dp) {
   if constexpr (QL < NQ) {
     constexpr int NG = NQ / 4, C = QL / MOE_SK_CH, QC = QL % MOE_SK_CH, NC = NQ / MOE_SK_CH, RP = MOE_SK_RP;
     const uint32_t *buf = lds + (C & 1) * MOE_SK_BUF_DW;
@@ -186,9 +194,10 @@ __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1
       u32x4_t a0, a1;
       dup_halves(r.w[P % RP], a0, a1);
       const int st = 4 * QC + 2 * j;  // block of the chunk
-      sk_step<QL & 3>(a0, e[2 * j], r.b, buf, st + 1, true, lane, sb, acc);
+      if (QL == 0 && j == 0) sk_step<QL & 3, false>(a0, e[2 * j], r.b, buf, st + 1, true, lane, sb, acc, rp, dp);
+      else sk_step<QL & 3, true>(a0, e[2 * j], r.b, buf, st + 1, true, lane, sb, acc, rp, dp);
       const bool last_of_chunk = QC + 1 == MOE_SK_CH && j == 1;
-      sk_step<QL & 3>(a1, e[2 * j + 1], r.b, buf, st + 2, !last_of_chunk, lane, sb, acc);
+      sk_step<QL & 3, true>(a1, e[2 * j + 1], r.b, buf, st + 2, !last_of_chunk, lane, sb, acc, rp, dp);
     }
     if constexpr (QC + 1 == MOE_SK_CH && C + 1 < NC) {
       // the next chunk has landed in LDS (this wave's loads, then everyone's)
@@ -200,7 +209,7 @@ __device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1
       load_skb_v(r.b, nb, lane, 0);
       load_skb_d(r.b, nb, lane, 0);
     }
-    sk_from<QL + 1, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, sb, acc);
+    sk_from<QL + 1, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, sb, acc, rp, dp);
   }
 }
 
@@ -231,7 +240,10 @@ __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao
   for (int e = 0; e < 16; e++) acc[e] = 0.0f;
   load_skb_v(r.b, lds, lane, 0);
   load_skb_d(r.b, lds, lane, 0);
-  sk_from<0, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, (lane >> 5) ? 127 : 131, acc);
+  f32x16_t rp;
+  float dp = 0.0f;
+  sk_from<0, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, (lane >> 5) ? 127 : 131, acc, rp, dp);
+  acc = acc + dp * rp;  // the last step's scaled sum
 }
 
 // gate/up -> clamp -> SwiGLU -> Q8_0(h) on items of up to 32 rows.  One
