@@ -1,29 +1,33 @@
 // kernels_stacked.h -- grouped gate/up and down on items of up to 32 rows,
 // the two Q8_0 digit planes stacked along K of one MFMA.
 //
-// v_mfma_scale_f32_32x32x64_f8f6f4 reduces 64 K per output column.  Here a
-// column is one token and its 64 K are one MXFP4 block twice: K 0-31 carry
-// the block's hi digits (B scale 2^4), K 32-63 its lo digits (B scale 2^0),
-// and both A lane halves (lane r + 32*ga, ga = 0, 1) hold the same weight
-// block of row r with its exponent.  Column n of the result is then
-// 2^(e_w - 127) times token n's exact integer block dot (16*hi + lo = q):
-// one MFMA is 32 rows x 32 tokens x one block with no zero half in B, and
-// each result value is scaled by its token's d once (16 FMAs per 32x32
-// block product; the octet kernels spend 16 per 32 rows x 8 tokens x 2
-// blocks).  Against an item of up to 32 rows one pass over the expert's
-// weights serves every row of the item, so an expert with 17-32 rows is
-// streamed once, not twice.
+// v_mfma_scale_f32_32x32x64_f8f6f4 reduces 64 K per output value.  Here A
+// is the item's tokens (A row t = token t) and B the weight tile (B column
+// r = weight row r), and the 64 K are one MXFP4 block twice: K 0-31 carry
+// the block's hi digits (A scale 2^4), K 32-63 its lo digits (A scale 2^0),
+// and both B lane halves (lane r + 32*gb, gb = 0, 1) hold the same weight
+// block of row r with its exponent.  D[t][r] is then 2^(e_w - 127) times
+// the exact integer block dot of token t and row r (16*hi + lo = q): one
+// MFMA is 32 tokens x 32 rows x one block with no zero half, and each
+// result value is scaled by its token's d once.  Against an item of up to
+// 32 rows one pass over the expert's weights serves every row of the item,
+// so an expert with 17-32 rows is streamed once, not twice.
 //
-// Operand lanes (the layouts the octet kernels use): A lane r + 32*ga holds
-// row r and K [32*ga, 32*ga + 32); the record layout gives lane (r, ga) block
-// 2j + ga of a quad in one load (step j), and v_permlane32_swap turns that
-// pair into [block 2j | block 2j] and [block 2j+1 | block 2j+1].  B lane
-// n + 32*gb holds column n: bytes 0-15 = K [16*gb, +16) (hi digits 16*gb ..
-// 16*gb + 15), bytes 16-31 = K [32 + 16*gb, +16) (lo digits, same offsets).
-// The B scale of lane n + 32*gb is that of K block gb (hi: 2^4, lo: 2^0).
-// D lane n + 32*gb holds column n, rows 8*i + 4*gb + j at element 4*i + j.
+// Tokens are A's rows so that a lane's 16 result values are 16 tokens of one
+// weight row (D lane r + 32*gb holds column r, tokens 8*i + 4*gb + j at
+// element 4*i + j): the d scaling of the tokens an item lacks is skipped
+// whole, 4 FMAs per 8 tokens (an item of 9-16 rows pays 8 FMAs per MFMA, not
+// 16), at the price of each lane reading its tokens' d as float4s.
 //
-// B is staged in LDS by chunks of MOE_SK_CH quads (8 blocks), double
+// Operand lanes (the layouts the octet kernels use): B lane r + 32*gb holds
+// weight row r and K [32*gb, 32*gb + 32); the record layout gives lane (r, gb)
+// block 2j + gb of a quad in one load (step j), and v_permlane32_swap turns
+// that pair into [block 2j | block 2j] and [block 2j+1 | block 2j+1].  A lane
+// t + 32*ga holds token t: bytes 0-15 = K [16*ga, +16) (hi digits 16*ga ..
+// 16*ga + 15), bytes 16-31 = K [32 + 16*ga, +16) (lo digits, same offsets).
+// The A scale of lane t + 32*ga is that of K block ga (hi: 2^4, lo: 2^0).
+//
+// A is staged in LDS by chunks of MOE_SK_CH quads (8 blocks), double
 // buffered, with direct global-to-LDS loads: per block, two 1 KiB runs (the
 // 64 lanes' bytes 0-15, then bytes 16-31, each lane 16 consecutive bytes,
 // so the operand reads are conflict-free), then the chunk's scales
@@ -41,6 +45,7 @@
 #define MOE_SK_SC_DW (MOE_SK_STEPS * MOE_SK_STEP_U4 * 4)  // dword offset of the scales in a chunk buffer
 #define MOE_SK_BUF_DW (MOE_SK_SC_DW + MOE_SK_STEPS * 32)  // dwords per chunk buffer (17 KiB)
 #define MOE_SK_LDS_BYTES (2 * MOE_SK_BUF_DW * 4)          // two chunk buffers (34 KiB)
+#define MOE_SK_DN_LDS_BYTES (MOE_SK_LDS_BYTES + MOE_SK_WAVES * 32 * 4)  // k_down_sk: + 32 router weights per wave
 #define MOE_SK_WAVES 8                          // waves per workgroup (one 32-row weight tile each)
 #define MOE_SK_RP 4  // weight ring, in block pairs (3 ahead: 3 KiB in flight per wave; 2 and 5 ahead measured the same)
 
@@ -67,8 +72,7 @@ __device__ __forceinline__ sdma make_sdma(int lane, int xr, int KB, bool block_m
 // w*SW + SW - 1 of the chunk (both halves; SW = blocks per wave) and the
 // scales of two blocks (waves below MOE_SK_STEPS/2): 2*SW + 1 loads or 2*SW.
 #define MOE_SK_SW (MOE_SK_STEPS / MOE_SK_WAVES)
-template <int C>
-__device__ __forceinline__ void sdma_issue(const sdma &g, const gsrc &src, uint32_t *buf, int wave) {
+__device__ __forceinline__ void sdma_issue(const sdma &g, const gsrc &src, uint32_t *buf, int wave, int C) {
   typedef __attribute__((address_space(3))) void *lds_t;
 #pragma unroll
   for (int i = 0; i < MOE_SK_SW; i++) {
@@ -83,10 +87,9 @@ __device__ __forceinline__ void sdma_issue(const sdma &g, const gsrc &src, uint3
                                              (MOE_SK_STEPS * C + 2 * wave) * g.bs4, 0, 0);
 }
 
-// One block's B operand and d of this lane, from a chunk buffer.
+// One block's A operand (the tokens' digits) of this lane, from a chunk buffer.
 struct skb {
   u32x4_t lo, hi;
-  float d;
 };
 
 __device__ __forceinline__ void load_skb_v(skb &b, const uint32_t *buf, int lane, int st) {
@@ -95,8 +98,22 @@ __device__ __forceinline__ void load_skb_v(skb &b, const uint32_t *buf, int lane
   b.hi = bl[(st * 2 + 1) * 64 + lane];
 }
 
-__device__ __forceinline__ void load_skb_d(skb &b, const uint32_t *buf, int lane, int st) {
-  b.d = reinterpret_cast<const float *>(buf + MOE_SK_SC_DW)[st * 32 + (lane & 31)];
+// The d of this lane's result tokens 8*i + 4*gb + (0..3), i < NK, of block
+// st of a chunk buffer (NK = the groups of 8 tokens that the item holds).
+template <int NK>
+__device__ __forceinline__ void load_skd(f32x4_t (&dq)[NK], const uint32_t *buf, int lane, int st) {
+  const f32x4_t *s = reinterpret_cast<const f32x4_t *>(buf + MOE_SK_SC_DW + st * 32 + 4 * (lane >> 5));
+#pragma unroll
+  for (int i = 0; i < NK; i++) dq[i] = s[2 * i];
+}
+
+// acc[4i + j] += dq[i][j] * r[4i + j] for the token groups i < NK.
+template <int NK>
+__device__ __forceinline__ void sk_scale(f32x16_t &acc, const f32x16_t &r, const f32x4_t (&dq)[NK]) {
+#pragma unroll
+  for (int i = 0; i < NK; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[4 * i + j] = __builtin_fmaf(dq[i][j], r[4 * i + j], acc[4 * i + j]);
 }
 
 // [x | x] and [y | y] from a register holding x in lanes 0-31, y in 32-63.
@@ -115,12 +132,20 @@ __device__ __forceinline__ void dup_halves1(uint32_t w, uint32_t &a0, uint32_t &
   a1 = p[1];
 }
 
-template <int NG>
 struct skring {
   u32x4_t w[MOE_SK_RP];  // block pair P in slot P % MOE_SK_RP (pair P = blocks 2P, 2P+1 of the stream)
-  uint32_t sc[NG][1][2];  // exponent dwords of each 4-quad group: lane (r, ga) holds block position 2j + ga
-  skb b;                 // the next step's B
+  uint32_t sc[1][2], scn[1][2];  // exponent dwords of this 4-quad group and the next: lane (r, gb) holds
+                                 // block position 2j + gb
+  skb b;                         // the next step's A
 };
+
+// Weight pair 8*G + SL of the stream (SL may reach into the next group).
+template <int CPOL>
+__device__ __forceinline__ void load_w32g(u32x4_t &w, const wstream (&ws)[1], const aoff32 &ao, int G, int SL) {
+  const int q = SL >> 1, j = SL & 1;
+  w = __builtin_amdgcn_raw_buffer_load_b128(ws[0].rec, ao.v + j * 512, (G + (q >> 2)) * MOE_REC_BYTES + (q & 3) * 1024,
+                                            CPOL);
+}
 
 // VMEM loads a wave issues after its chunk-C staging loads up to the end of
 // chunk C: the next group's 2 exponent dwords, and the weight pairs issued
@@ -136,114 +161,161 @@ __host__ __device__ constexpr int sdma_after() {
   return n;
 }
 
-// One MFMA step (block position POS of quad QL, block st of the chunk),
-// software-pipelined by one step: the MFMA goes out into its own result
-// registers, then the next step's digits are read from LDS, then the
-// previous step's result is scaled by its d into acc (PREV) while this MFMA
-// runs, then the next d.  The scaled sums reach acc in block order, as
-// without the pipelining; sk_loop adds the last step's after the loop.
-template <int SEL, bool PREV>
-__device__ __forceinline__ void sk_step(const u32x4_t &a4, uint32_t sa, skb &b, const uint32_t *nbuf, int nst,
-                                        bool next, int lane, int sb, f32x16_t &acc, f32x16_t &rp, float &dp) {
-  const i32x8_t a = {(int)a4.x, (int)a4.y, (int)a4.z, (int)a4.w, 0, 0, 0, 0};
-  const i32x8_t bv = {(int)b.lo.x, (int)b.lo.y, (int)b.lo.z, (int)b.lo.w,
+// One MFMA step (block st of the chunk buffer cbuf), software-pipelined by
+// one step: the MFMA goes out into its own result registers, then the next
+// step's digits are read from LDS (nbuf, block nst), then the previous
+// step's result is scaled by its tokens' d into acc while this MFMA runs,
+// then this step's d is read for the next step's scaling.  The scaled sums
+// reach acc in block order; sk_loop adds the last step's after the loop.
+// w4, sw: the weight block (both lane halves) and its exponent dword (byte
+// SEL); sa: the digits' scale (2^4 hi, 2^0 lo).
+template <int SEL, int NK>
+__device__ __forceinline__ void sk_step(const u32x4_t &w4, uint32_t sw, skb &b, const uint32_t *cbuf, int st,
+                                        const uint32_t *nbuf, int nst, bool next, int lane, int sa, f32x16_t &acc,
+                                        f32x16_t &rp, f32x4_t (&dq)[NK]) {
+  const i32x8_t wv = {(int)w4.x, (int)w4.y, (int)w4.z, (int)w4.w, 0, 0, 0, 0};
+  const i32x8_t xv = {(int)b.lo.x, (int)b.lo.y, (int)b.lo.z, (int)b.lo.w,
                       (int)b.hi.x, (int)b.hi.y, (int)b.hi.z, (int)b.hi.w};
   f32x16_t z;
 #pragma unroll
   for (int e = 0; e < 16; e++) z[e] = 0.0f;
-  const f32x16_t r = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(a, bv, z, 4, 0, SEL, (int)sa, 0, sb);
-  const float d = b.d;
+  const f32x16_t r = __builtin_amdgcn_mfma_scale_f32_32x32x64_f8f6f4(xv, wv, z, 0, 4, 0, sa, SEL, (int)sw);
   __builtin_amdgcn_sched_barrier(0);
   if (next) load_skb_v(b, nbuf, lane, nst);
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (PREV) {
-    acc = acc + dp * rp;
-    asm volatile("" : "+v"(acc));
-  }
+  sk_scale<NK>(acc, rp, dq);
+  asm volatile("" : "+v"(acc));
   __builtin_amdgcn_sched_barrier(0);
   rp = r;
-  dp = d;
-  if (next) load_skb_d(b, nbuf, lane, nst);
+  load_skd<NK>(dq, cbuf, lane, st);
 }
 
-// Quads QL .. NQ-1 of the K loop (weights loaded with cache policy CPOL).
-template <int QL, int NQ, int CPOL>
-__device__ __forceinline__ void sk_from(skring<NQ / 4> &r, const wstream (&ws)[1], const aoff32 &ao,
-                                        const gsrc &src, const sdma &g, uint32_t *lds, int wave, int lane, int sb,
-                                        f32x16_t &acc, f32x16_t &rp, float &dp) {
-  if constexpr (QL < NQ) {
-    constexpr int NG = NQ / 4, C = QL / MOE_SK_CH, QC = QL % MOE_SK_CH, NC = NQ / MOE_SK_CH, RP = MOE_SK_RP;
-    const uint32_t *buf = lds + (C & 1) * MOE_SK_BUF_DW;
-    if constexpr (QC == 0 && C + 1 < NC) {  // the next chunk's staging, straight into the other buffer
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      sdma_issue<C + 1>(g, src, lds + ((C + 1) & 1) * MOE_SK_BUF_DW, wave);
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    if constexpr ((QL & 3) == 0 && QL / 4 + 1 < NG) load_sc32<1>(r.sc[QL / 4 + 1], ws, ao, QL / 4 + 1);
-    uint32_t e[4];  // this quad's group exponents, every lane block position 0..3
-    dup_halves1(r.sc[QL / 4][0][0], e[0], e[1]);
-    dup_halves1(r.sc[QL / 4][0][1], e[2], e[3]);
+// Quad QL (0..3) of the 4-quad group G of the K loop; the group's chunks
+// 2G and 2G + 1 are in buffers 0 and 1.  Every group but the last (LAST: G
+// == NQ/4 - 1, known at compile time) runs the same code from a rolled loop:
+// it stages the chunk after each of its chunks, loads the next group's
+// exponents, keeps the weight ring 3 pairs ahead, and each chunk end waits
+// for exactly the next chunk's staging (a constant count of younger loads).
+// Weights are loaded with cache policy CPOL.
+template <int QL, int NQ, int CPOL, int NK, bool LAST>
+__device__ __forceinline__ void sk_quad(skring &r, const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
+                                        const sdma &g, uint32_t *lds, int wave, int lane, int sa, int G,
+                                        f32x16_t &acc, f32x16_t &rp, f32x4_t (&dq)[NK]) {
+  constexpr int NG = NQ / 4, RP = MOE_SK_RP, c = QL >> 1, qc = QL & 1;  // chunk of the group, quad of the chunk
+  static_assert(MOE_SK_CH == 2 && RP == 4, "a group is two chunks of two quads, the ring 4 pairs");
+  constexpr bool next_chunk = !LAST || c == 0;  // chunk 2G + c + 1 exists
+  const uint32_t *buf = lds + c * MOE_SK_BUF_DW;
+  if constexpr (qc == 0 && next_chunk) {  // the next chunk's staging, straight into the other buffer
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    sdma_issue(g, src, lds + (c ^ 1) * MOE_SK_BUF_DW, wave, 2 * G + c + 1);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  if constexpr (QL == 0 && !LAST) load_sc32<1>(r.scn, ws, ao, G + 1);
+  uint32_t e[4];  // this quad's group exponents, every lane block position 0..3
+  dup_halves1(r.sc[0][0], e[0], e[1]);
+  dup_halves1(r.sc[0][1], e[2], e[3]);
 #pragma unroll
-    for (int j = 0; j < 2; j++) {
-      const int P = 2 * QL + j;
-      if (P + RP - 1 < 2 * NQ) load_w32step<CPOL>(r.w[(P + RP - 1) % RP], ws, ao, P + RP - 1);
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      u32x4_t a0, a1;
-      dup_halves(r.w[P % RP], a0, a1);
-      const int st = 4 * QC + 2 * j;  // block of the chunk
-      if (QL == 0 && j == 0) sk_step<QL & 3, false>(a0, e[2 * j], r.b, buf, st + 1, true, lane, sb, acc, rp, dp);
-      else sk_step<QL & 3, true>(a0, e[2 * j], r.b, buf, st + 1, true, lane, sb, acc, rp, dp);
-      const bool last_of_chunk = QC + 1 == MOE_SK_CH && j == 1;
-      sk_step<QL & 3, true>(a1, e[2 * j + 1], r.b, buf, st + 2, !last_of_chunk, lane, sb, acc, rp, dp);
-    }
-    if constexpr (QC + 1 == MOE_SK_CH && C + 1 < NC) {
-      // the next chunk has landed in LDS (this wave's loads, then everyone's)
-      asm volatile("" ::: "memory");
-      __builtin_amdgcn_sched_barrier(0);
-      __builtin_amdgcn_s_waitcnt(vmcnt_imm(sdma_after<C, NQ>()));
-      const uint32_t *nb = lds + ((C + 1) & 1) * MOE_SK_BUF_DW;
-      lds_barrier();
-      load_skb_v(r.b, nb, lane, 0);
-      load_skb_d(r.b, nb, lane, 0);
-    }
-    sk_from<QL + 1, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, sb, acc, rp, dp);
+  for (int j = 0; j < 2; j++) {
+    const int SL = 2 * QL + j + RP - 1;  // the pair 3 ahead, from the group's first pair
+    if (!LAST || SL < 8) load_w32g<CPOL>(r.w[SL % RP], ws, ao, G, SL);
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4_t w0, w1;
+    dup_halves(r.w[(2 * QL + j) % RP], w0, w1);
+    const int st = 4 * qc + 2 * j;  // block of the chunk
+    sk_step<QL, NK>(w0, e[2 * j], r.b, buf, st, buf, st + 1, true, lane, sa, acc, rp, dq);
+    const bool last_of_chunk = qc == 1 && j == 1;
+    sk_step<QL, NK>(w1, e[2 * j + 1], r.b, buf, st + 1, buf, st + 2, !last_of_chunk, lane, sa, acc, rp, dq);
+  }
+  if constexpr (qc == 1 && next_chunk) {
+    // the next chunk has landed in LDS (this wave's loads, then everyone's)
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_imm(sdma_after<(LAST ? 2 * (NG - 1) : 0) + c, NQ>()));
+    lds_barrier();
+    load_skb_v(r.b, lds + (c ^ 1) * MOE_SK_BUF_DW, lane, 0);
+  }
+}
+
+template <int NQ, int CPOL, int NK, bool LAST>
+__device__ __forceinline__ void sk_group(skring &r, const wstream (&ws)[1], const aoff32 &ao, const gsrc &src,
+                                         const sdma &g, uint32_t *lds, int wave, int lane, int sa, int G,
+                                         f32x16_t &acc, f32x16_t &rp, f32x4_t (&dq)[NK]) {
+  sk_quad<0, NQ, CPOL, NK, LAST>(r, ws, ao, src, g, lds, wave, lane, sa, G, acc, rp, dq);
+  sk_quad<1, NQ, CPOL, NK, LAST>(r, ws, ao, src, g, lds, wave, lane, sa, G, acc, rp, dq);
+  sk_quad<2, NQ, CPOL, NK, LAST>(r, ws, ao, src, g, lds, wave, lane, sa, G, acc, rp, dq);
+  sk_quad<3, NQ, CPOL, NK, LAST>(r, ws, ao, src, g, lds, wave, lane, sa, G, acc, rp, dq);
+  if constexpr (!LAST) {
+    r.sc[0][0] = r.scn[0][0];
+    r.sc[0][1] = r.scn[0][1];
   }
 }
 
 // The K loop of one wave: its 32-row weight tile over NQ quads against the
-// 32 staged tokens (xr: the staged row of token lane&31, < 0 absent).
-// acc: lane n + 32*gb, element 4i + j = token n, row 8i + 4gb + j.  CPOL:
-// the weights' cache policy (non-temporal where no other item reads them).
-template <int NQ, int CPOL>
+// 32 staged tokens (xr: the staged row of token lane&31, < 0 absent).  acc:
+// lane r + 32*gb, element 4i + j = weight row r, token 8i + 4gb + j (left 0
+// for the groups i >= NK, which hold no token of the item).  CPOL: the
+// weights' cache policy (non-temporal where no other item reads them).
+template <int NQ, int CPOL, int NK>
 __device__ __forceinline__ void sk_loop(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src, int xr, int KB,
                                         bool block_major, int n_rows, uint32_t *lds, int wave, int lane,
                                         f32x16_t &acc) {
-  static_assert(NQ % MOE_SK_CH == 0, "whole chunks");
+  static_assert(NQ % 4 == 0 && NQ >= 8, "whole groups, at least two");
   const sdma g = make_sdma(lane, xr, KB, block_major, n_rows);
-  skring<NQ / 4> r;
-  sdma_issue<0>(g, src, lds, wave);
+  skring r;
+  sdma_issue(g, src, lds, wave, 0);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
-  load_sc32<1>(r.sc[0], ws, ao, 0);
+  load_sc32<1>(r.sc, ws, ao, 0);
 #pragma unroll
-  for (int i = 0; i + 1 < MOE_SK_RP; i++)
-    if (i < 2 * NQ) load_w32step<CPOL>(r.w[i], ws, ao, i);
+  for (int i = 0; i + 1 < MOE_SK_RP; i++) load_w32g<CPOL>(r.w[i], ws, ao, 0, i);
   asm volatile("" ::: "memory");
   __builtin_amdgcn_sched_barrier(0);
   // chunk 0 has landed (2 exponent dwords and the first weight pairs went out after it)
-  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 + (MOE_SK_RP - 1 < 2 * NQ ? MOE_SK_RP - 1 : 2 * NQ)));
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(2 + MOE_SK_RP - 1));
   lds_barrier();
-#pragma unroll
-  for (int e = 0; e < 16; e++) acc[e] = 0.0f;
-  load_skb_v(r.b, lds, lane, 0);
-  load_skb_d(r.b, lds, lane, 0);
   f32x16_t rp;
-  float dp = 0.0f;
-  sk_from<0, NQ, CPOL>(r, ws, ao, src, g, lds, wave, lane, (lane >> 5) ? 127 : 131, acc, rp, dp);
-  acc = acc + dp * rp;  // the last step's scaled sum
+  f32x4_t dq[NK];
+#pragma unroll
+  for (int e = 0; e < 16; e++) {
+    acc[e] = 0.0f;
+    rp[e] = 0.0f;  // the first step scales a zero result: acc stays +0
+  }
+#pragma unroll
+  for (int i = 0; i < NK; i++) dq[i] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+  load_skb_v(r.b, lds, lane, 0);
+  const int sa = (lane >> 5) ? 127 : 131;
+#pragma unroll 1
+  for (int G = 0; G + 1 < NQ / 4; G++) sk_group<NQ, CPOL, NK, false>(r, ws, ao, src, g, lds, wave, lane, sa, G, acc, rp, dq);
+  sk_group<NQ, CPOL, NK, true>(r, ws, ao, src, g, lds, wave, lane, sa, NQ / 4 - 1, acc, rp, dq);
+  sk_scale<NK>(acc, rp, dq);  // the last step's scaled sums
+}
+
+// sk_loop for the item's nk = ceil(rows / 8) groups of 8 tokens and weight
+// cache policy (split: the default policy, else non-temporal).
+template <int NQ>
+__device__ __forceinline__ void sk_loop_any(const wstream (&ws)[1], const aoff32 &ao, const gsrc &src, int xr,
+                                            int KB, bool block_major, int n_rows, uint32_t *lds, int wave, int lane,
+                                            int nk, bool split, f32x16_t &acc) {
+#define MOE_SK_LOOP(CP, K) sk_loop<NQ, CP, K>(ws, ao, src, xr, KB, block_major, n_rows, lds, wave, lane, acc)
+  if (split) {
+    switch (nk) {
+      case 1: MOE_SK_LOOP(0, 1); break;
+      case 2: MOE_SK_LOOP(0, 2); break;
+      case 3: MOE_SK_LOOP(0, 3); break;
+      default: MOE_SK_LOOP(0, 4); break;
+    }
+  } else {
+    switch (nk) {
+      case 1: MOE_SK_LOOP(MOE_CPOL_NT, 1); break;
+      case 2: MOE_SK_LOOP(MOE_CPOL_NT, 2); break;
+      case 3: MOE_SK_LOOP(MOE_CPOL_NT, 3); break;
+      default: MOE_SK_LOOP(MOE_CPOL_NT, 4); break;
+    }
+  }
+#undef MOE_SK_LOOP
 }
 
 // gate/up -> clamp -> SwiGLU -> Q8_0(h) on items of up to 32 rows.  One
@@ -272,16 +344,16 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
   const gsrc src = make_gsrc(xq, xd, T, KB);
   const int n = lane & 31, gb = lane >> 5;
   const int xr = n < nt ? (shared ? row0 + n - P : perm[row0 + n] / k) : -1;
+  const int nk = __builtin_amdgcn_readfirstlane((nt + 7) >> 3);
   f32x16_t acc;
   // an expert of one item reads its tiles once: non-temporal, as in decode;
   // the items of a larger expert share them through L2
-  if (it.w & MOE_ITEM_SPLIT) sk_loop<NQ, 0>(ws, ao, src, xr, KB, false, T, lds, wave, lane, acc);
-  else sk_loop<NQ, MOE_CPOL_NT>(ws, ao, src, xr, KB, false, T, lds, wave, lane, acc);
+  sk_loop_any<NQ>(ws, ao, src, xr, KB, false, T, lds, wave, lane, nk, (it.w & MOE_ITEM_SPLIT) != 0, acc);
   lds_barrier();  // every wave is done with the chunk buffers
   float *red = reinterpret_cast<float *>(lds);  // [unit][gate/up][token][row]
 #pragma unroll
   for (int e = 0; e < 16; e++)
-    red[(((wave & 3) * 2 + (wave >> 2)) * 32 + n) * MOE_UNIT + 8 * (e >> 2) + 4 * gb + (e & 3)] = acc[e];
+    red[(((wave & 3) * 2 + (wave >> 2)) * 32 + 8 * (e >> 2) + 4 * gb + (e & 3)) * MOE_UNIT + n] = acc[e];
   __syncthreads();
   // (unit, token) c = 16*round + 2*wave + half-wave: unit c / 32, token c % 32
 #pragma unroll
@@ -304,7 +376,7 @@ void k_gate_up_sk(const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w
 // per (256 rows of H, item), wave = one 32-row tile of H over all of F
 // against the item's h rows; y[row] = the tile's rows x the pair's router
 // weight (the shared expert's rows unweighted).  grid (H/256, item
-// capacity), 512 threads, LDS MOE_SK_LDS_BYTES.  Requires F == 128 * NQ,
+// capacity), 512 threads, LDS MOE_SK_DN_LDS_BYTES.  Requires F == 128 * NQ,
 // NQ % 4 == 0, H % 256 == 0.
 template <int NQ>
 __global__ __launch_bounds__(64 * MOE_SK_WAVES) __attribute__((amdgpu_waves_per_eu(4)))
@@ -324,19 +396,26 @@ void k_down_sk(const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs,
   const aoff32 ao = make_aoff32(lane, NQ4);
   const gsrc src = make_gsrc(hs, hd, n_rows, KB);
   const int n = lane & 31, gb = lane >> 5;
-  const bool live = n < nt;
+  const int nk = __builtin_amdgcn_readfirstlane((nt + 7) >> 3);
   f32x16_t acc;
-  if (it.w & MOE_ITEM_SPLIT) sk_loop<NQ, 0>(ws, ao, src, live ? row0 + n : -1, KB, true, n_rows, lds, wave, lane, acc);
-  else sk_loop<NQ, MOE_CPOL_NT>(ws, ao, src, live ? row0 + n : -1, KB, true, n_rows, lds, wave, lane, acc);
-  const int rr = row0 + (live ? n : 0);
-  const float wt = (live && !shared) ? wts[perm[rr]] : 1.0f;
-  float v[16];
+  const int xr = n < nt ? row0 + n : -1;
+  sk_loop_any<NQ>(ws, ao, src, xr, KB, true, n_rows, lds, wave, lane, nk, (it.w & MOE_ITEM_SPLIT) != 0, acc);
+  // the router weight of token n, then of this lane's result tokens through
+  // the wave's own 32 floats past the chunk buffers
+  float *wtl = reinterpret_cast<float *>(lds + 2 * MOE_SK_BUF_DW) + 32 * wave;
+  const float wt = (n < nt && !shared) ? wts[perm[row0 + n]] : 1.0f;
+  if (gb == 0) wtl[n] = wt;
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  const f32x4_t *wq = reinterpret_cast<const f32x4_t *>(wtl + 4 * gb);
+  float *dst = y + (size_t)row0 * H + (size_t)t32 * 32 + n;
 #pragma unroll
-  for (int e = 0; e < 16; e++) v[e] = shared ? acc[e] : __fmul_rn(acc[e], wt);
-  if (live) {
-    float *dst = y + (size_t)rr * H + (size_t)t32 * 32 + 4 * gb;
+  for (int i = 0; i < 4; i++) {
+    if (i >= nk) break;
+    const f32x4_t w4 = wq[2 * i];
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      *reinterpret_cast<float4 *>(dst + 8 * i) = make_float4(v[4 * i], v[4 * i + 1], v[4 * i + 2], v[4 * i + 3]);
+    for (int j = 0; j < 4; j++) {
+      const int t = 8 * i + 4 * gb + j;
+      if (t < nt) dst[(size_t)t * H] = shared ? acc[4 * i + j] : __fmul_rn(acc[4 * i + j], w4[j]);
+    }
   }
 }

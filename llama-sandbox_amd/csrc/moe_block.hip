@@ -405,13 +405,15 @@ extern "C" moe_status moe_ctx_create(int device, uint64_t budget_bytes, moe_ctx 
       delete c;
       return MOE_ERR_NO_DEVICE;
     }
-  // and the stacked-digit kernels (two 17 KiB chunk buffers, 34 KiB; set for uniformity)
-  const void *sk_kernels[] = {(const void *)k_gate_up_sk<56>, (const void *)k_gate_up_sk<48>,
-                              (const void *)k_gate_up_sk<32>, (const void *)k_gate_up_sk<16>,
-                              (const void *)k_down_sk<24>, (const void *)k_down_sk<16>, (const void *)k_down_sk<12>,
-                              (const void *)k_down_sk<8>};
-  for (const void *kf : sk_kernels)
-    if (hipFuncSetAttribute(kf, hipFuncAttributeMaxDynamicSharedMemorySize, MOE_SK_LDS_BYTES) != hipSuccess) {
+  // and the stacked-digit kernels (two 17 KiB chunk buffers, 34 KiB, and
+  // down's router weights; set for uniformity)
+  const std::pair<const void *, int> sk_kernels[] = {
+      {(const void *)k_gate_up_sk<56>, MOE_SK_LDS_BYTES},   {(const void *)k_gate_up_sk<48>, MOE_SK_LDS_BYTES},
+      {(const void *)k_gate_up_sk<32>, MOE_SK_LDS_BYTES},   {(const void *)k_gate_up_sk<16>, MOE_SK_LDS_BYTES},
+      {(const void *)k_down_sk<24>, MOE_SK_DN_LDS_BYTES}, {(const void *)k_down_sk<16>, MOE_SK_DN_LDS_BYTES},
+      {(const void *)k_down_sk<12>, MOE_SK_DN_LDS_BYTES}, {(const void *)k_down_sk<8>, MOE_SK_DN_LDS_BYTES}};
+  for (const auto &kf : sk_kernels)
+    if (hipFuncSetAttribute(kf.first, hipFuncAttributeMaxDynamicSharedMemorySize, kf.second) != hipSuccess) {
       delete c;
       return MOE_ERR_NO_DEVICE;
     }
@@ -937,10 +939,10 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
     const bool dn2 = o2 && !sk && H % (32 * MOE_DOL2_WAVES) == 0;
     const dim3 b2(64 * MOE_DOL2_WAVES);
 #define MOE_DN_ARGS16 L.m[T_DOWN].w, s.hq, s.hd, P + T, items16, perm, wts, F, H, s.y
-    if (sk && F == 128 * 16) hipLaunchKernelGGL(k_down_sk<16>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
-    else if (sk && F == 128 * 24) hipLaunchKernelGGL(k_down_sk<24>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
-    else if (sk && F == 128 * 12) hipLaunchKernelGGL(k_down_sk<12>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
-    else if (sk && F == 128 * 8) hipLaunchKernelGGL(k_down_sk<8>, gdo2, b2, MOE_SK_LDS_BYTES, st, MOE_DN_ARGS16);
+    if (sk && F == 128 * 16) hipLaunchKernelGGL(k_down_sk<16>, gdo2, b2, MOE_SK_DN_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (sk && F == 128 * 24) hipLaunchKernelGGL(k_down_sk<24>, gdo2, b2, MOE_SK_DN_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (sk && F == 128 * 12) hipLaunchKernelGGL(k_down_sk<12>, gdo2, b2, MOE_SK_DN_LDS_BYTES, st, MOE_DN_ARGS16);
+    else if (sk && F == 128 * 8) hipLaunchKernelGGL(k_down_sk<8>, gdo2, b2, MOE_SK_DN_LDS_BYTES, st, MOE_DN_ARGS16);
     else if (dn2 && F == 128 * 6) hipLaunchKernelGGL(k_down_ol2<6>, gdo2, b2, lo2, st, MOE_DN_ARGS16);
     else if (oct && F == 128 * 16) hipLaunchKernelGGL(k_down_ol<16>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
     else if (oct && F == 128 * 6) hipLaunchKernelGGL(k_down_ol<6>, gdo, dim3(256), lo, st, MOE_DN_ARGS);
