@@ -116,14 +116,18 @@ def cpu_baseline(seconds: float, threads: int, seed: int):
     L = oracle.OracleLayer.generated(seed, 0, sh.hidden, sh.ffn, sh.n_expert, sh.n_used, experts=experts,
                                      shared=True)
     log(f"cpu baseline: generated {len(experts)} experts + shared in {time.time() - t0:.1f}s")
-    L.forward(xs[:1], ids[:1], wts[:1], n_threads=threads)  # warm-up
+    # the eight-row (AVX2) path: bit-identical with the scalar checker, which is checked here once
+    ref = L.forward(xs[:1], ids[:1], wts[:1], n_threads=threads)["out"]
+    if not np.array_equal(L.forward_rows8(xs[:1], ids[:1], wts[:1], n_threads=threads).view(np.uint32),
+                          ref.view(np.uint32)):
+        raise SystemExit("bench: the CPU baseline's eight-row path differs from the oracle")
     times = []
     t_start = time.perf_counter()
     i = 0
     while time.perf_counter() - t_start < seconds or len(times) < 3:
         t = i % n_tok
         a = time.perf_counter()
-        L.forward(xs[t:t + 1], ids[t:t + 1], wts[t:t + 1], n_threads=threads)
+        L.forward_rows8(xs[t:t + 1], ids[t:t + 1], wts[t:t + 1], n_threads=threads)
         times.append(time.perf_counter() - a)
         i += 1
     med = float(np.median(times)) * 1e6
@@ -133,7 +137,8 @@ def cpu_baseline(seconds: float, threads: int, seed: int):
         f"{threads} threads ({hc})")
     return {"value": round(med, 1), "unit": "us/token", "cores": threads, "kind": "port",
             "sample": f"{len(times)} V3 decode tokens (T=1, top-8 + shared, {n_tok} independent routings), "
-                      f"oracle/libmoe_oracle.so on {threads} threads, median per token",
+                      f"oracle/libmoe_oracle.so's eight-row path ({'AVX2' if oracle.simd_available() else 'scalar'}, "
+                      f"bit-identical with the scalar oracle) on {threads} threads, median per token",
             "gbps": round(touched / med / 1e3, 2), "cpu_model": hc["model"], "cpus_visible": hc["visible"],
             "cpus_affinity": hc["affinity"], "cpu_quota": hc["quota"]}
 

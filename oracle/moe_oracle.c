@@ -9,6 +9,7 @@
  */
 #include "moe_oracle.h"
 
+#include <immintrin.h>
 #include <math.h>
 #include <pthread.h>
 #include <stdlib.h>
@@ -150,6 +151,66 @@ float mo_vec_dot_mxfp4_q8_0(int K, const uint8_t *wrow, const int8_t *qs,
   return acc;
 }
 
+/* Eight rows at once (row i at w + i*stride), each bit for bit
+ * mo_vec_dot_mxfp4_q8_0: the per-block integer sums are exact in any order,
+ * and the f32 work -- s = fp16(d) * e8m0_half(e), acc = acc + s * isum, in
+ * ascending block order -- is the same IEEE multiply and add per row, done
+ * in eight lanes.  AVX2 where the CPU has it: the nibbles index a vpshufb
+ * table of the doubled e2m1 values, |w| x (q with w's sign) goes through
+ * vpmaddubsw / vpmaddwd (|w| <= 12, |q| <= 127: no int16 saturation; q is
+ * never -128 here, Q8_0 codes are within +-127), and three vphaddd levels
+ * turn the rows' eight partial sums into one int32 each.  This is the
+ * CPU-baseline's inner loop only; the checker keeps the scalar path. */
+__attribute__((target("avx2"))) static void vec_dot8_avx2(int K, const uint8_t *w, size_t stride,
+                                                           const int8_t *qs, const uint16_t *d, float *out) {
+  const __m256i lut = _mm256_setr_epi8(0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12,
+                                       0, 1, 2, 3, 4, 6, 8, 12, 0, -1, -2, -3, -4, -6, -8, -12);
+  const __m256i m4 = _mm256_set1_epi8(0x0f);
+  const __m256i ones = _mm256_set1_epi16(1);
+  const __m256i two = _mm256_set1_epi32(2), one = _mm256_set1_epi32(1);
+  const __m256i den = _mm256_set1_epi32(0x00200000);
+  __m256 acc = _mm256_setzero_ps();
+  for (int b = 0; b < K / MO_QK; b++) {
+    const __m256i qv = _mm256_loadu_si256((const __m256i *)(qs + (size_t)b * MO_QK));
+    const uint8_t *b0 = w + (size_t)b * MO_MXFP4_BYTES;
+    __m256i part[8];
+    for (int r = 0; r < 8; r++) {
+      /* the 16 nibble bytes in both halves: low nibbles index half 0, high half 1 */
+      const __m256i v = _mm256_broadcastsi128_si256(_mm_loadu_si128((const __m128i *)(b0 + (size_t)r * stride + 1)));
+      const __m256i idx = _mm256_blend_epi32(_mm256_and_si256(v, m4), _mm256_and_si256(_mm256_srli_epi16(v, 4), m4), 0xF0);
+      const __m256i wv = _mm256_shuffle_epi8(lut, idx);
+      const __m256i p16 = _mm256_maddubs_epi16(_mm256_sign_epi8(wv, wv), _mm256_sign_epi8(qv, wv));
+      part[r] = _mm256_madd_epi16(p16, ones);
+    }
+    const __m256i t01 = _mm256_hadd_epi32(part[0], part[1]), t23 = _mm256_hadd_epi32(part[2], part[3]);
+    const __m256i t45 = _mm256_hadd_epi32(part[4], part[5]), t67 = _mm256_hadd_epi32(part[6], part[7]);
+    const __m256i t03 = _mm256_hadd_epi32(t01, t23), t47 = _mm256_hadd_epi32(t45, t67);
+    /* t03 = [r0 r1 r2 r3 | r0 r1 r2 r3] over the two 128-bit halves of the block */
+    const __m256i isum = _mm256_add_epi32(_mm256_permute2x128_si256(t03, t47, 0x20),
+                                          _mm256_permute2x128_si256(t03, t47, 0x31));
+    /* mo_e8m0_half of the eight rows' exponents, as bit patterns */
+    const __m256i e = _mm256_setr_epi32(b0[0], b0[stride], b0[2 * stride], b0[3 * stride], b0[4 * stride],
+                                        b0[5 * stride], b0[6 * stride], b0[7 * stride]);
+    const __m256i big = _mm256_slli_epi32(_mm256_sub_epi32(e, one), 23);
+    const __m256i small = _mm256_sllv_epi32(den, e);
+    const __m256i bits = _mm256_blendv_epi8(big, small, _mm256_cmpgt_epi32(two, e));
+    const __m256 sc = _mm256_mul_ps(_mm256_set1_ps(mo_fp16_to_fp32(d[b])), _mm256_castsi256_ps(bits));
+    acc = _mm256_add_ps(acc, _mm256_mul_ps(sc, _mm256_cvtepi32_ps(isum)));
+  }
+  _mm256_storeu_ps(out, acc);
+}
+
+int mo_simd_available(void) { return __builtin_cpu_supports("avx2") ? 1 : 0; }
+
+void mo_vec_dot8_mxfp4_q8_0(int K, const uint8_t *w, size_t stride, const int8_t *qs, const uint16_t *d,
+                            float *out) {
+  if (mo_simd_available()) {
+    vec_dot8_avx2(K, w, stride, qs, d, out);
+    return;
+  }
+  for (int r = 0; r < 8; r++) out[r] = mo_vec_dot_mxfp4_q8_0(K, w + (size_t)r * stride, qs, d);
+}
+
 /* ------------------------------------------------------------------------ */
 /* routing                                                                  */
 /* ------------------------------------------------------------------------ */
@@ -266,6 +327,7 @@ typedef struct {
   int8_t *hq;     /* [P+T][F] */
   uint16_t *hd;   /* [P+T][F/32] */
   float *y;       /* [P+T][H] weighted routed rows, then shared rows */
+  int rows8;      /* the dot products eight rows at a time (mo_vec_dot8_mxfp4_q8_0) */
   pthread_barrier_t bar;
 } fwd_state;
 
@@ -299,6 +361,38 @@ static void *fwd_worker(void *argp) {
   /* gate / up / clamp / SwiGLU for every (expert row, ffn column) */
   span((size_t)R * F, a->tid, S->nthreads, &b, &e);
   for (size_t i = b; i < e && S->h_in; i++) S->h[i] = S->h_in[i];
+  if (S->rows8 && !S->h_in) {
+    /* the same per column, eight ffn columns per dot call */
+    span((size_t)R * (F / 8), a->tid, S->nthreads, &b, &e);
+    for (size_t i = b; i < e; i++) {
+      const int r = (int)(i / (size_t)(F / 8)), c0 = (int)(i % (size_t)(F / 8)) * 8;
+      const uint8_t *gw, *uw;
+      int t;
+      if (r < P) {
+        t = r / k;
+        gw = L->gate[S->ids[r]];
+        uw = L->up[S->ids[r]];
+      } else {
+        t = r - P;
+        gw = L->sh_gate;
+        uw = L->sh_up;
+      }
+      const int8_t *q = S->xq + (size_t)t * H;
+      const uint16_t *d = S->xd + (size_t)t * (H / MO_QK);
+      float g8[8], u8[8];
+      mo_vec_dot8_mxfp4_q8_0(H, gw + (size_t)c0 * gu_row, gu_row, q, d, g8);
+      mo_vec_dot8_mxfp4_q8_0(H, uw + (size_t)c0 * gu_row, gu_row, q, d, u8);
+      for (int j = 0; j < 8; j++) {
+        float g = g8[j], u = u8[j];
+        if (L->clamp > 1e-6f) {
+          u = clampf(u, -L->clamp, L->clamp);
+          g = clampf(g, -INFINITY, L->clamp);
+        }
+        S->h[(size_t)r * F + c0 + j] = (g / (1.0f + expf(-g))) * u;
+      }
+    }
+    b = e = 0;  /* the per-column loop below has nothing left */
+  }
   for (size_t i = b; i < e && !S->h_in; i++) {
     const int r = (int)(i / (size_t)F), c = (int)(i % (size_t)F);
     const uint8_t *gw, *uw;
@@ -336,6 +430,18 @@ static void *fwd_worker(void *argp) {
 
   /* down, times the router weight for routed rows (the MUL node) */
   span((size_t)R * H, a->tid, S->nthreads, &b, &e);
+  if (S->rows8) {
+    span((size_t)R * (H / 8), a->tid, S->nthreads, &b, &e);
+    for (size_t i = b; i < e; i++) {
+      const int r = (int)(i / (size_t)(H / 8)), c0 = (int)(i % (size_t)(H / 8)) * 8;
+      const uint8_t *dw = r < P ? L->down[S->ids[r]] : L->sh_down;
+      float v8[8];
+      mo_vec_dot8_mxfp4_q8_0(F, dw + (size_t)c0 * dn_row, dn_row, S->hq + (size_t)r * F,
+                             S->hd + (size_t)r * (F / MO_QK), v8);
+      for (int j = 0; j < 8; j++) S->y[(size_t)r * H + c0 + j] = r < P ? v8[j] * S->wts[r] : v8[j];
+    }
+    b = e = 0;
+  }
   for (size_t i = b; i < e; i++) {
     const int r = (int)(i / (size_t)H), c = (int)(i % (size_t)H);
     const uint8_t *dw = r < P ? L->down[S->ids[r]] + (size_t)c * dn_row
@@ -361,24 +467,24 @@ static void *fwd_worker(void *argp) {
 
 static int forward_impl(const mo_layer *L, int T, const float *x, const int32_t *ids, const float *wts,
                         const float *h_in, float *out, float *per_slot, float *h_routed, float *h_shared,
-                        int n_threads);
+                        int n_threads, int rows8);
 
 int mo_moe_forward_taps(const mo_layer *L, int T, const float *x,
                         const int32_t *ids, const float *wts, float *out,
                         float *per_slot, float *h_routed, float *h_shared,
                         int n_threads) {
-  return forward_impl(L, T, x, ids, wts, NULL, out, per_slot, h_routed, h_shared, n_threads);
+  return forward_impl(L, T, x, ids, wts, NULL, out, per_slot, h_routed, h_shared, n_threads, 0);
 }
 
 int mo_moe_forward_from_h(const mo_layer *L, int T, const int32_t *ids, const float *wts,
                           const float *h, float *out, float *per_slot, int n_threads) {
   if (!h) return -1;
-  return forward_impl(L, T, NULL, ids, wts, h, out, per_slot, NULL, NULL, n_threads);
+  return forward_impl(L, T, NULL, ids, wts, h, out, per_slot, NULL, NULL, n_threads, 0);
 }
 
 static int forward_impl(const mo_layer *L, int T, const float *x, const int32_t *ids, const float *wts,
                         const float *h_in, float *out, float *per_slot, float *h_routed, float *h_shared,
-                        int n_threads) {
+                        int n_threads, int rows8) {
   if (!L || T <= 0 || (!x && !h_in) || !ids || !wts || !out) return -1;
   if (L->H % MO_QK || L->F % MO_QK || L->k <= 0 || L->E <= 0) return -1;
   for (int p = 0; p < T * L->k; p++) {
@@ -401,6 +507,7 @@ static int forward_impl(const mo_layer *L, int T, const float *x, const int32_t 
   S.ids = ids;
   S.wts = wts;
   S.out = out;
+  S.rows8 = rows8 && F % 8 == 0 && H % 8 == 0;
   S.xq = (int8_t *)malloc((size_t)T * H);
   S.xd = (uint16_t *)malloc(sizeof(uint16_t) * (size_t)T * (H / MO_QK));
   S.h = (float *)malloc(sizeof(float) * (size_t)R * F);
@@ -441,6 +548,11 @@ int mo_moe_forward(const mo_layer *L, int T, const float *x,
                    const int32_t *ids, const float *wts, float *out,
                    float *per_slot, int n_threads) {
   return mo_moe_forward_taps(L, T, x, ids, wts, out, per_slot, NULL, NULL, n_threads);
+}
+
+int mo_moe_forward_rows8(const mo_layer *L, int T, const float *x, const int32_t *ids, const float *wts,
+                         float *out, int n_threads) {
+  return forward_impl(L, T, x, ids, wts, NULL, out, NULL, NULL, NULL, n_threads, 1);
 }
 
 /* ------------------------------------------------------------------------ */

@@ -57,6 +57,13 @@ void mo_quantize_q8_0(const float *x, int K, int8_t *qs, uint16_t *d);
 /* Exact int32 dot of one MXFP4 block with one Q8_0 block. */
 int32_t mo_block_isum(const uint8_t *wblock, const int8_t *q);
 
+/* mo_vec_dot_mxfp4_q8_0 of eight rows (row i at w + i*stride) against one
+ * Q8_0 vector, bit for bit per row; AVX2 when mo_simd_available(), else the
+ * scalar routine per row.  Codes must lie in [-127, 127] (Q8_0's range). */
+void mo_vec_dot8_mxfp4_q8_0(int K, const uint8_t *w, size_t stride, const int8_t *qs, const uint16_t *d,
+                            float *out);
+int mo_simd_available(void);
+
 /* ggml_vec_dot_mxfp4_q8_0, generic order: acc += (fp16(d)*e8m0_half(e))*isum
  * over blocks in ascending order, f32. */
 float mo_vec_dot_mxfp4_q8_0(int K, const uint8_t *wrow, const int8_t *qs,
@@ -113,6 +120,14 @@ typedef struct {
 int mo_moe_forward(const mo_layer *L, int T, const float *x,
                    const int32_t *ids, const float *wts, float *out,
                    float *per_slot, int n_threads);
+
+/* mo_moe_forward with the dot products eight output rows at a time
+ * (mo_vec_dot8_mxfp4_q8_0): the same result bit for bit, faster.  The
+ * CPU-baseline leg of bench.py times this; the checker uses mo_moe_forward.
+ * F and H must be multiples of 8 for the eight-row loops (else the
+ * per-row path runs). */
+int mo_moe_forward_rows8(const mo_layer *L, int T, const float *x, const int32_t *ids, const float *wts,
+                         float *out, int n_threads);
 
 /* Intermediate taps for tests: h (post-SwiGLU, pre-quantization) [T][k][F]
  * and the shared expert's h [T][F] (may be NULL). */

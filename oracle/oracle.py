@@ -81,6 +81,11 @@ def lib():
         L.mo_moe_forward_from_h.restype = ctypes.c_int
         L.mo_moe_forward_from_h.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _i32p, _f32p, _f32p, _f32p,
                                             _f32p, ctypes.c_int]
+        L.mo_moe_forward_rows8.restype = ctypes.c_int
+        L.mo_moe_forward_rows8.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _f32p, _i32p, _f32p, _f32p,
+                                           ctypes.c_int]
+        L.mo_vec_dot8_mxfp4_q8_0.argtypes = [ctypes.c_int, _u8p, ctypes.c_size_t, _i8p, _u16p, _f32p]
+        L.mo_simd_available.restype = ctypes.c_int
         L.mo_moe_h_exact.restype = ctypes.c_int
         L.mo_moe_h_exact.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _f32p, _i32p, _f64p, _f64p,
                                      ctypes.c_int]
@@ -96,6 +101,24 @@ def lib():
 
 def _p(a: np.ndarray, t):
     return a.ctypes.data_as(t)
+
+
+def vec_dot8(blocks: np.ndarray, qs: np.ndarray, d: np.ndarray) -> np.ndarray:
+    """mo_vec_dot8_mxfp4_q8_0 over 8 rows of MXFP4 blocks [8, K/32, 17]
+    against one Q8_0 vector (qs int8 [K], d fp16 bits [K/32])."""
+    blocks = np.ascontiguousarray(blocks, np.uint8)
+    qs = np.ascontiguousarray(qs, np.int8)
+    d = np.ascontiguousarray(d, np.uint16)
+    assert blocks.shape[0] == 8 and blocks.shape[2] == 17
+    K = blocks.shape[1] * 32
+    out = np.empty(8, np.float32)
+    lib().mo_vec_dot8_mxfp4_q8_0(K, _p(blocks, _u8p), blocks.shape[1] * 17, _p(qs, _i8p), _p(d, _u16p),
+                                 _p(out, _f32p))
+    return out
+
+
+def simd_available() -> bool:
+    return bool(lib().mo_simd_available())
 
 
 # ---- formats -----------------------------------------------------------------
@@ -262,6 +285,22 @@ class OracleLayer:
             res["h"] = hr
             res["h_shared"] = hs
         return res
+
+    def forward_rows8(self, x: np.ndarray, ids: np.ndarray, wts: np.ndarray, n_threads: int = 1) -> np.ndarray:
+        """forward()'s out, bit for bit, with the dot products eight rows at
+        a time (AVX2 where present): the CPU baseline's path."""
+        x = np.ascontiguousarray(x, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        wts = np.ascontiguousarray(wts, np.float32)
+        T = x.shape[0]
+        out = np.empty((T, self.H), np.float32)
+        s, keep = self._struct()
+        rc = lib().mo_moe_forward_rows8(ctypes.byref(s), T, _p(x, _f32p), _p(ids, _i32p), _p(wts, _f32p),
+                                        _p(out, _f32p), int(n_threads))
+        del keep
+        if rc != 0:
+            raise ValueError("oracle forward rejected its arguments")
+        return out
 
     def h_exact(self, x: np.ndarray, ids: np.ndarray, n_threads: int = 1):
         """The SwiGLU output with gate/up summed exactly in float64 (same

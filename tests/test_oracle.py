@@ -290,6 +290,39 @@ def test_forward_thread_count_invariant(oracle):
     np.testing.assert_array_equal(a, b)
 
 
+def test_vec_dot8_bit_exact_with_vec_dot(oracle):
+    # the CPU baseline's eight-row dot against the scalar one, row by row:
+    # random nibbles, codes at both ends of Q8_0's range, denormal and large
+    # block scales, zero d
+    rng = np.random.default_rng(41)
+    for K in (32, 256, 7168):
+        nb = K // 32
+        for trial in range(4):
+            rows = rng.integers(0, 256, (8, nb, 17), dtype=np.uint8)
+            rows[:, :, 0] = rng.choice([0, 1, 2, 100, 127, 128, 140, 200], (8, nb))
+            qs = rng.integers(-127, 128, K).astype(np.int8)
+            qs[: min(K, 40)] = np.resize(np.array([127, -127], np.int8), min(K, 40))
+            d = np.array([oracle.fp32_to_fp16_bits(float(v)) for v in rng.uniform(1e-4, 0.5, nb)], np.uint16)
+            d[trial % nb] = 0
+            got = oracle.vec_dot8(rows, qs, d)
+            for r in range(8):
+                want = np.float32(oracle.vec_dot(rows[r:r + 1], qs, d))
+                assert got[r].view(np.uint32) == want.view(np.uint32), (K, trial, r, got[r], want)
+
+
+@pytest.mark.parametrize("shared,clamp,threads", [(False, 0.0, 1), (True, 0.0, 3), (True, 0.75, 8)])
+def test_forward_rows8_bit_exact_with_forward(oracle, shared, clamp, threads):
+    H, F, E, k, T = 256, 128, 8, 4, 5
+    L = _tiny_layer(oracle, 37, H, F, E, k, shared, clamp)
+    rng = np.random.default_rng(38)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    wts = rng.uniform(0.1, 0.4, (T, k)).astype(np.float32)
+    a = L.forward(x, ids, wts, n_threads=1)["out"]
+    b = L.forward_rows8(x, ids, wts, n_threads=threads)
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+
+
 # ---- generator ----------------------------------------------------------------------
 
 def test_mix64_known_answer(oracle):
