@@ -149,7 +149,7 @@ __device__ __forceinline__ void load_w32g(u32x4_t &w, const wstream (&ws)[1], co
 
 // VMEM loads a wave issues after its chunk-C staging loads up to the end of
 // chunk C: the next group's 2 exponent dwords, and the weight pairs issued
-// during the chunk's 8 pairs (3 ahead).
+// during the chunk's 4 pairs (3 ahead).
 template <int C, int NQ>
 __host__ __device__ constexpr int sdma_after() {
   int n = 0;
