@@ -565,7 +565,8 @@ typedef struct {
   const int32_t *ids;
   const int8_t *xq;
   const uint16_t *xd;
-  double *h; /* [R][F] */
+  double *h;     /* [R][F] */
+  double *bound; /* [R][F] or NULL: the error bound of an f32 evaluation instead of h */
 } hx_arg;
 
 /* One row of gate or up in double: every block term isum * e8m0_half(e) *
@@ -577,6 +578,26 @@ static double dot_exact(int K, const uint8_t *wrow, const int8_t *qs, const uint
     const uint8_t *blk = wrow + (size_t)b * MO_MXFP4_BYTES;
     acc += (double)mo_block_isum(blk, qs + (size_t)b * MO_QK) * (double)mo_e8m0_half(blk[0]) *
            (double)mo_fp16_to_fp32(d[b]);
+  }
+  return acc;
+}
+
+/* The magnitude sum behind one row's dot, for its error bound: sum over the
+ * blocks of e8m0_half(e) * fp16(d) * sum_j (|q_j| + 30) * |w_j|.  The device
+ * multiplies the weights by the two e4m3 digit planes of q (q = 16*hi + lo,
+ * lo in [0, 15]), so its block terms are bounded by |16*hi| + |lo| <= |q| +
+ * 30 times |w|; every product is exact and every block's integer sum too. */
+static double dot_l1(int K, const uint8_t *wrow, const int8_t *qs, const uint16_t *d) {
+  double acc = 0.0;
+  for (int b = 0; b < K / MO_QK; b++) {
+    const uint8_t *blk = wrow + (size_t)b * MO_MXFP4_BYTES;
+    const int8_t *q = qs + (size_t)b * MO_QK;
+    int32_t s = 0;
+    for (int j = 0; j < 16; j++) {
+      s += (abs(q[j]) + 30) * abs(mo_kvalues[blk[1 + j] & 0x0f]);
+      s += (abs(q[j + 16]) + 30) * abs(mo_kvalues[blk[1 + j] >> 4]);
+    }
+    acc += (double)s * (double)mo_e8m0_half(blk[0]) * fabs((double)mo_fp16_to_fp32(d[b]));
   }
   return acc;
 }
@@ -603,13 +624,41 @@ static void *hx_worker(void *argp) {
       u = u > -l ? u : -l;
       g = g < l ? g : l;
     }
-    a->h[i] = g / (1.0 + exp(-g)) * u;
+    const double h = g / (1.0 + exp(-g)) * u;
+    if (!a->bound) {
+      a->h[i] = h;
+      continue;
+    }
+    /* Any f32 evaluation that sums the exact block terms in any order, with
+     * at most one rounding per term and per addition: |error| <= gamma_m *
+     * (sum of |terms|), m = blocks + 8 (Higham, Accuracy and Stability of
+     * Numerical Algorithms, 2nd ed., eq. 4.4); the clamps are 1-Lipschitz,
+     * |silu'| <= 1.1; SiLU's exp, add, divide and the product add at most 8
+     * roundings of h.  Twice that, first order plus the product term. */
+    const double uu = ldexp(1.0, -24), m = (double)(H / MO_QK + 8), gam = m * uu / (1.0 - m * uu);
+    const double eg = gam * dot_l1(H, gw + (size_t)c * gu_row, q, d);
+    const double eu = gam * dot_l1(H, uw + (size_t)c * gu_row, q, d);
+    const double s = g / (1.0 + exp(-g));
+    a->bound[i] = 2.0 * (1.1 * eg * fabs(u) + fabs(s) * eu + 1.1 * eg * eu + 8.0 * uu * fabs(h)) + 1e-37;
   }
   return NULL;
 }
 
+static int h_exact_impl(const mo_layer *L, int T, const float *x, const int32_t *ids, double *h_routed,
+                        double *h_shared, int n_threads, int bound);
+
 int mo_moe_h_exact(const mo_layer *L, int T, const float *x, const int32_t *ids, double *h_routed,
                    double *h_shared, int n_threads) {
+  return h_exact_impl(L, T, x, ids, h_routed, h_shared, n_threads, 0);
+}
+
+int mo_moe_h_bound(const mo_layer *L, int T, const float *x, const int32_t *ids, double *b_routed,
+                   double *b_shared, int n_threads) {
+  return h_exact_impl(L, T, x, ids, b_routed, b_shared, n_threads, 1);
+}
+
+static int h_exact_impl(const mo_layer *L, int T, const float *x, const int32_t *ids, double *h_routed,
+                        double *h_shared, int n_threads, int bound) {
   if (!L || T <= 0 || !x || !ids || !h_routed) return -1;
   if (L->H % MO_QK || L->F % MO_QK || L->k <= 0 || L->E <= 0) return -1;
   for (int p = 0; p < T * L->k; p++)
@@ -629,7 +678,7 @@ int mo_moe_h_exact(const mo_layer *L, int T, const float *x, const int32_t *ids,
   for (int t = 0; t < T; t++)
     mo_quantize_q8_0(x + (size_t)t * H, H, xq + (size_t)t * H, xd + (size_t)t * (H / MO_QK));
   for (int i = 0; i < n_threads; i++) {
-    args[i] = (hx_arg){L, T, P, R, n_threads, i, ids, xq, xd, h};
+    args[i] = (hx_arg){L, T, P, R, n_threads, i, ids, xq, xd, bound ? NULL : h, bound ? h : NULL};
     if (i) pthread_create(&th[i], NULL, hx_worker, &args[i]);
   }
   hx_worker(&args[0]);

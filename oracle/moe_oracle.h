@@ -152,6 +152,16 @@ int mo_moe_forward_from_h(const mo_layer *L, int T, const int32_t *ids, const fl
 int mo_moe_h_exact(const mo_layer *L, int T, const float *x, const int32_t *ids,
                    double *h_routed, double *h_shared, int n_threads);
 
+/* For each value of that h, a bound on the error of any f32 evaluation of
+ * it that sums the block terms of gate and up in any order (one rounding
+ * per term and per addition at most, the device's digit-plane split of
+ * each term included) and then evaluates clamp, SiLU and the product in
+ * f32: |h_f32 - h_exact| <= bound.  Same layout and arguments as
+ * mo_moe_h_exact.  The parity checker's yardstick for single values whose
+ * gate or up sum cancels (large terms, small result). */
+int mo_moe_h_bound(const mo_layer *L, int T, const float *x, const int32_t *ids,
+                   double *b_routed, double *b_shared, int n_threads);
+
 /* ---- synthetic weights ------------------------------------------------ */
 
 /* SplitMix64 finalizer (Steele, Lea, Flood 2014). */

@@ -89,6 +89,9 @@ def lib():
         L.mo_moe_h_exact.restype = ctypes.c_int
         L.mo_moe_h_exact.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _f32p, _i32p, _f64p, _f64p,
                                      ctypes.c_int]
+        L.mo_moe_h_bound.restype = ctypes.c_int
+        L.mo_moe_h_bound.argtypes = [ctypes.POINTER(_Layer), ctypes.c_int, _f32p, _i32p, _f64p, _f64p,
+                                     ctypes.c_int]
         L.mo_mix64.restype = ctypes.c_uint64
         L.mo_mix64.argtypes = [ctypes.c_uint64]
         L.mo_gen_key.restype = ctypes.c_uint64
@@ -319,6 +322,23 @@ class OracleLayer:
         if rc != 0:
             raise ValueError("oracle h_exact rejected its arguments")
         return hr, hs
+
+    def h_bound(self, x: np.ndarray, ids: np.ndarray, n_threads: int = 1):
+        """Per value of h_exact's h, a bound on the error of any f32
+        evaluation that sums the gate/up block terms in any order (same
+        layout as h_exact: [T, k, F], shared [T, F] or None)."""
+        x = np.ascontiguousarray(x, np.float32)
+        ids = np.ascontiguousarray(ids, np.int32)
+        T = x.shape[0]
+        br = np.empty((T, self.k, self.F), np.float64)
+        bs = np.empty((T, self.F), np.float64) if self.shared else None
+        s, keep = self._struct()
+        rc = lib().mo_moe_h_bound(ctypes.byref(s), T, _p(x, _f32p), _p(ids, _i32p), _p(br, _f64p),
+                                  None if bs is None else _p(bs, _f64p), int(n_threads))
+        del keep
+        if rc != 0:
+            raise ValueError("oracle h_bound rejected its arguments")
+        return br, bs
 
     def forward_from_h(self, ids: np.ndarray, wts: np.ndarray, h: np.ndarray, h_shared=None,
                        n_threads: int = 1, per_slot: bool = False):

@@ -261,6 +261,68 @@ def test_h_exact_vs_float64(oracle, shared, clamp):
     assert 0 < np.max(np.abs(f32 - h)) <= 1e-5 * scale
 
 
+@pytest.mark.parametrize("clamp", [0.0, 2.0])
+def test_h_bound_covers_other_orders_and_catches_a_dropped_term(oracle, clamp):
+    """The checker's per-value f32 bound (h_bound) holds for f32 evaluations
+    in orders other than the oracle's (the block terms summed in reverse, and
+    pairwise, in numpy float32; the oracle's own h), and is tight enough that
+    losing the largest block term of gate puts every value outside it whose
+    h that loss moves by more than twice the bound -- most values, where no
+    clamp hides it."""
+    H, F, E, k, T = 1024, 64, 4, 2, 3
+    L = _tiny_layer(oracle, 43, H, F, E, k, False, clamp, e_lo=126 if clamp else 122, e_span=4)
+    rng = np.random.default_rng(44)
+    x = rng.standard_normal((T, H)).astype(np.float32)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int32)
+    h, _ = L.h_exact(x, ids)
+    b, _ = L.h_bound(x, ids)
+    f32 = L.forward(x, ids, np.ones((T, k), np.float32), taps=True)["h"]
+    assert np.all(np.abs(f32.astype(np.float64) - h) <= b)
+    xq, xd = oracle.quantize_q8_0(x)
+    xa = np_ref.q8_dequant(xq, xd)  # [T, H] float64, exact
+    nb = H // 32
+
+    def act(g, u):  # clamp and SwiGLU in float32
+        if clamp:
+            u = np.clip(u, np.float32(-clamp), np.float32(clamp))
+            g = np.minimum(g, np.float32(clamp))
+        return (g / (np.float32(1) + np.exp(-g))) * u
+
+    caught = total = 0
+    for t in range(T):
+        for s in range(k):
+            G, U = (np_ref.dequant_blocks(m) for m in (L.gate[ids[t, s]], L.up[ids[t, s]]))
+            tg = (G * xa[t]).reshape(F, nb, 32).sum(-1)  # [F, nb] exact block terms
+            tu = (U * xa[t]).reshape(F, nb, 32).sum(-1)
+            for order in ("reverse", "pairwise"):
+                if order == "reverse":
+                    g32 = np.zeros(F, np.float32)
+                    u32 = np.zeros(F, np.float32)
+                    for j in reversed(range(nb)):
+                        g32 = g32 + tg[:, j].astype(np.float32)
+                        u32 = u32 + tu[:, j].astype(np.float32)
+                else:
+                    g32, u32 = tg.astype(np.float32), tu.astype(np.float32)
+                    while g32.shape[1] > 1:
+                        g32 = g32[:, 0::2] + g32[:, 1::2]
+                        u32 = u32[:, 0::2] + u32[:, 1::2]
+                    g32, u32 = g32[:, 0], u32[:, 0]
+                assert np.all(np.abs(act(g32, u32).astype(np.float64) - h[t, s]) <= b[t, s]), (t, s, order)
+            # the largest term of gate lost: values where that changes h by
+            # more than twice the bound in exact arithmetic (a clamp can hide
+            # it) must all fall outside the bound in f32
+            jg = np.argmax(np.abs(tg), axis=1)
+            g_drop64 = tg.sum(1) - tg[np.arange(F), jg]
+            err = np.abs(act(g_drop64.astype(np.float32), tu.sum(1).astype(np.float32)).astype(np.float64) - h[t, s])
+            shift = np.abs(np_ref.swiglu(g_drop64, tu.sum(1), clamp) - h[t, s])
+            visible = shift > 2 * b[t, s]
+            caught += int(np.sum((err > b[t, s]) & visible))
+            total += int(np.sum(visible))
+            if not clamp:  # unclamped, most values show the lost term (not those where up is near 0)
+                assert np.sum(visible) >= 0.7 * F, (t, s, int(np.sum(visible)))
+    assert total > 0 and caught == total, (caught, total)
+
+
 def test_forward_clamp_engages(oracle):
     # large weights make |g|, |u| far exceed a small limit: output must differ from unclamped
     H, F, E, k, T = 64, 64, 4, 2, 2

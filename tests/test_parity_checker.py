@@ -49,16 +49,17 @@ def test_rejects_a_uniform_h_error_under_the_old_gate(oracle):
 
 
 def test_rejects_one_bad_row(oracle):
-    """One h row of 320 (token 2, slot 1) with an error in a single 32-block,
-    about 8x that row's own f32 error: diluted below the call-level gate,
-    caught by the per-row gate."""
+    """One h row of 320 (token 2, slot 1) with a shift of 4x that row's own
+    RMS f32 error on a single 32-block: every value still within the f32
+    error bound of some summation order and the shift diluted below the
+    call-level gate, but caught by the per-row gate."""
     shape, L, x, ids, wts, ref = _case(oracle, T=64)
     h, hs = ref["h"].copy(), ref["h_shared"].copy()
     h64, _ = L.h_exact(x, ids, n_threads=4)
     e_row = float(np.sqrt(np.mean((ref["h"][2, 1].astype(np.float64) - h64[2, 1]) ** 2)))
     e_row = max(e_row, 2.0 ** -24 * float(np.sqrt(np.mean(h64[2, 1] ** 2))))
     row = h[2, 1]
-    row[64:96] += np.float32(4 * 8 * e_row)  # 32 of 512 values: a quarter of the shift in row RMS
+    row[64:96] += np.float32(4 * e_row)  # 32 of 512 values
     out = L.forward_from_h(ids, wts, h, hs, n_threads=4)
     with pytest.raises(AssertionError, match="in row"):
         check_block(oracle, L, Taps(h, hs), shape, x, ids, wts, out, "planted row", n_threads=4)
@@ -76,10 +77,10 @@ def test_rejects_code_flips_beyond_f32_order(oracle):
     # move each value halfway to the next code's center: a different code almost everywhere
     h = (ref["h"] + 0.6 * step * np.sign(ref["h"])).astype(np.float32)
     out = L.forward_from_h(ids, wts, h, ref["h_shared"], n_threads=4)
-    saved = parity.H_CALL_FACTOR, parity.H_ROW_FACTOR
-    parity.H_CALL_FACTOR = parity.H_ROW_FACTOR = 1e30
+    saved = parity.H_VALUE_FACTOR, parity.H_CALL_FACTOR, parity.H_ROW_FACTOR
+    parity.H_VALUE_FACTOR = parity.H_CALL_FACTOR = parity.H_ROW_FACTOR = 1e30
     try:
         with pytest.raises(AssertionError, match="code differences"):
             check_block(oracle, L, Taps(h, ref["h_shared"]), shape, x, ids, wts, out, "planted flips", n_threads=4)
     finally:
-        parity.H_CALL_FACTOR, parity.H_ROW_FACTOR = saved
+        parity.H_VALUE_FACTOR, parity.H_CALL_FACTOR, parity.H_ROW_FACTOR = saved
