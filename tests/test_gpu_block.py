@@ -382,6 +382,38 @@ def test_shape_sweep(blk, torch_dev, oracle, case):
         blk.release_layer(lid)
 
 
+# ---- seeded random shapes: H, F, E, top-k, T, shared, clamp and routing drawn at random -----
+
+def _random_case(i):
+    rng = np.random.default_rng(8100 + i)
+    H = int(rng.choice([1024, 2048, 3072, 4096, 5120, 6144, 7168]))
+    F = int(rng.choice([512, 768, 1024, 1536, 2048, 3072]))
+    E = int(rng.choice([8, 16, 32, 64, 128, 256]))
+    k = int(rng.integers(1, min(8, E) + 1))
+    T = int(rng.choice([1, 2, 3, 4, 5, 8, 13, 16, 31, 40, 64, 100, 200]))
+    return H, F, E, k, T, bool(rng.integers(0, 2)), float(rng.choice([0.0, 0.0, 2.0, 6.0])), \
+        int(rng.choice([wl.ROUTE_SOFTMAX, wl.ROUTE_SIGMOID, wl.ROUTE_SQRT_SOFTPLUS]))
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("case", range(40))
+def test_random_shapes(blk, torch_dev, oracle, case):
+    """Shapes off every curated list, against the oracle with the same gates."""
+    H, F, E, k, T, sh, clamp, route = _random_case(case)
+    shape = wl.LayerShape(hidden=H, ffn=F, n_expert=E, n_used=k, has_shared=sh, route_mode=route, clamp=clamp)
+    say(f"random case {case}: H={H} F={F} E={E} k={k} T={T} shared={sh} clamp={clamp} route={route}")
+    lid = 600 + case
+    blk.generate_layer(lid, shape, seed=5000 + case)
+    try:
+        x, lg = wl.make_inputs(shape, T, 170 + case)
+        ids, wts = oracle.route(lg, k, route, norm=True)
+        got = run_block(blk, torch_dev, lid, x, ids, wts)
+        check_block(oracle, oracle_layer(oracle, shape, 5000 + case, lid, ids), blk, shape, x, ids, wts, got,
+                    f"random {case}")
+    finally:
+        blk.release_layer(lid)
+
+
 # ---- the ggml backend's split, computed through moe_split_compute -----------------------------
 
 @pytest.mark.parametrize("T", [1, 5])
