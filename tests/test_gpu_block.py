@@ -382,6 +382,29 @@ def test_shape_sweep(blk, torch_dev, oracle, case):
         blk.release_layer(lid)
 
 
+# ---- the grouping's limits: many tokens, many experts --------------------------------------------
+
+@pytest.mark.slow
+@pytest.mark.parametrize("H, F, E, k, T, route", [
+    (1024, 1024, 64, 8, 2048, wl.ROUTE_SIGMOID),    # 16384 pairs, 256 rows per expert: stacked, many split items
+    (1024, 512, 1024, 8, 96, wl.ROUTE_SOFTMAX),     # the largest expert count (10-bit ids), octets
+    (2048, 1024, 1024, 16, 4, wl.ROUTE_SOFTMAX),    # top-16 over 1024 experts, pairs with 17 slots
+])
+def test_grouping_limits(blk, torch_dev, oracle, H, F, E, k, T, route):
+    shape = wl.LayerShape(hidden=H, ffn=F, n_expert=E, n_used=k, has_shared=True, route_mode=route)
+    say(f"limits: H={H} F={F} E={E} k={k} T={T}")
+    lid = 700
+    blk.generate_layer(lid, shape, seed=711)
+    try:
+        x, lg = wl.make_inputs(shape, T, 712)
+        ids, wts = oracle.route(lg, k, route, norm=True)
+        got = run_block(blk, torch_dev, lid, x, ids, wts)
+        check_block(oracle, oracle_layer(oracle, shape, 711, lid, ids), blk, shape, x, ids, wts, got,
+                    f"limits E={E} T={T}")
+    finally:
+        blk.release_layer(lid)
+
+
 # ---- seeded random shapes: H, F, E, top-k, T, shared, clamp and routing drawn at random -----
 
 def _random_case(i):
