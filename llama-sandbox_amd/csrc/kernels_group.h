@@ -224,6 +224,175 @@ __global__ __launch_bounds__(1024) void k_group(const int32_t *__restrict__ ids,
 }
 
 // ---------------------------------------------------------------------------
+// k_group for calls of at most MOE_GF_PAIRS pairs, on one wave: the same
+// outputs (counts and offsets only when counts != NULL).  The pairs are
+// NPL = ceil(P / 64) chunks of 64 (at most 2), lane l holding pair 64*i + l
+// of each chunk i.
+//   1. ballots of each chunk's valid lanes and of each id bit;
+//   2. a pair walks each chunk's ballots from the top id bit down, which
+//      gives the chunk's lanes with its id (eq) and with a smaller id (lt);
+//      row = (valid pairs with a smaller id) + (pairs with its id before it)
+//      is k_group's grouped row: experts ascending, pairs ascending within
+//      an expert;
+//   3. the first pair of an expert holds the expert's item count ceil(c/BT);
+//      ballots of the bits of those counts give every first pair the items
+//      of all smaller experts, i.e. the index of its first item.
+// All in registers: no LDS, no barrier, no table over the experts and no
+// scan, and short executed code (a launch this small is bound by latency,
+// instruction fetch included).  Workgroups 1..: Q8_0 of x as in k_group,
+// MOE_GF_QBLOCKS blocks each.
+// grid 1 + ceil(n_xblocks / MOE_GF_QBLOCKS), 256 threads (wave 0 of
+// workgroup 0 groups).
+#define MOE_GF_NPL 2
+#define MOE_GF_PAIRS (64 * MOE_GF_NPL)
+#define MOE_GF_QBLOCKS 128
+
+// Bits needed for values in [0, n] (n >= 0).
+__device__ __forceinline__ int gf_bits(int n) { return n > 0 ? 32 - __clz(n) : 1; }
+
+// Ballots of one chunk: bb[b] = lanes whose valid id has bit b set, v =
+// lanes with a valid id (ids below 2^10).
+__device__ __forceinline__ void chunk_ballots(int e, bool ok, uint64_t (&bb)[10], uint64_t &v) {
+  v = __ballot(ok);
+#pragma unroll
+  for (int b = 0; b < 10; b++) bb[b] = __ballot(ok && ((e >> b) & 1));
+}
+
+// The lanes of a chunk with id e (eq) and with a valid smaller id (lt), from
+// the chunk's ballots (0 <= e < 2^10).  Straight-line code: bits above the
+// largest id only cost their 9 instructions, less than a branch around them.
+__device__ __forceinline__ void chunk_rank(const uint64_t (&bb)[10], uint64_t v, int e, uint64_t &eq, uint64_t &lt) {
+  eq = v;
+  lt = 0ull;
+#pragma unroll
+  for (int b = 9; b >= 0; b--) {
+    const uint64_t B = bb[b];
+    const bool one = (e >> b) & 1;
+    lt |= one ? (eq & ~B) : 0ull;
+    eq &= one ? B : ~B;
+  }
+}
+
+template <int NPL>
+__device__ __forceinline__ void group_one_wave(const int32_t *__restrict__ ids, int P, int E, int T, int shared,
+                                               int BT, int32_t *__restrict__ counts, int32_t *__restrict__ offsets,
+                                               int32_t *__restrict__ perm, int32_t *__restrict__ inv,
+                                               int32_t *__restrict__ items, int BT2, int32_t *__restrict__ items2) {
+  const int lane = threadIdx.x;
+  int e[NPL];
+  bool ok[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    e[i] = 64 * i + lane < P ? ids[64 * i + lane] : -1;
+    ok[i] = e[i] >= 0 && e[i] < E;
+  }
+  const uint64_t below = (1ull << lane) - 1ull;
+  uint64_t ltm[NPL][NPL];  // [own pair][chunk]
+  int less[NPL], before[NPL], cnt[NPL];
+#pragma unroll
+  for (int i = 0; i < NPL; i++) less[i] = before[i] = cnt[i] = 0;
+#pragma unroll
+  for (int c = 0; c < NPL; c++) {  // one chunk's ballots alive at a time
+    uint64_t bb[10], v;
+    chunk_ballots(e[c], ok[c], bb, v);
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+      uint64_t eq, lt;
+      chunk_rank(bb, v, ok[i] ? e[i] : 0, eq, lt);
+      ltm[i][c] = lt;
+      less[i] += __popcll(lt);
+      cnt[i] += __popcll(eq);
+      before[i] += c < i ? __popcll(eq) : (c == i ? __popcll(eq & below) : 0);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NPL; i++) {
+    const int p = 64 * i + lane;
+    if (ok[i]) {
+      perm[less[i] + before[i]] = p;
+      if (inv) inv[p] = less[i] + before[i];
+    } else if (inv && p < P) {
+      inv[p] = -1;  // dropped pair: no grouped row
+    }
+  }
+  if (counts) {  // per expert: pairs with its id, valid pairs with a smaller id
+    uint64_t cb[NPL][10], cv[NPL];  // the ballots are taken with every lane active, before the loop
+#pragma unroll
+    for (int c = 0; c < NPL; c++) chunk_ballots(e[c], ok[c], cb[c], cv[c]);
+    for (int ex = lane; ex < E; ex += 64) {
+      int ce = 0, le = 0;
+#pragma unroll
+      for (int c = 0; c < NPL; c++) {
+        uint64_t q, l;
+        chunk_rank(cb[c], cv[c], ex, q, l);
+        ce += __popcll(q);
+        le += __popcll(l);
+      }
+      counts[ex] = ce;
+      offsets[ex] = le;
+    }
+    int n = 0;
+#pragma unroll
+    for (int c = 0; c < NPL; c++) n += __popcll(__ballot(ok[c]));
+    if (lane == 0) offsets[E] = n;
+  }
+  for (int li = 0; li < 2; li++) {
+    int32_t *list = li ? items2 : items;
+    if (!list) continue;
+    const int bt = li ? BT2 : BT;
+    int n[NPL], base[NPL], tot = 0;
+#pragma unroll
+    for (int i = 0; i < NPL; i++) {
+      n[i] = ok[i] && before[i] == 0 ? (cnt[i] + bt - 1) / bt : 0;  // first pair of its expert
+      base[i] = 0;
+    }
+    const int nbits = gf_bits((P + bt - 1) / bt);
+    for (int b = 0; b < nbits; b++) {
+#pragma unroll
+      for (int c = 0; c < NPL; c++) {
+        const uint64_t m = __ballot((n[c] >> b) & 1);
+        tot += __popcll(m) << b;
+#pragma unroll
+        for (int i = 0; i < NPL; i++) base[i] += __popcll(ltm[i][c] & m) << b;
+      }
+    }
+    int4 *rec = reinterpret_cast<int4 *>(list) + 1;
+#pragma unroll
+    for (int i = 0; i < NPL; i++)
+      for (int j = 0; j < n[i]; j++) {
+        const int r = j * bt;
+        rec[base[i] + j] = make_int4(e[i], less[i] + r, cnt[i] - r < bt ? cnt[i] - r : bt, n[i] > 1 ? MOE_ITEM_SPLIT : 0);
+      }
+    const int ns = shared ? (T + bt - 1) / bt : 0;  // the shared expert's items follow the routed ones
+    for (int j = lane; j < ns; j += 64) {
+      const int r = j * bt;
+      rec[tot + j] = make_int4(E, P + r, T - r < bt ? T - r : bt, MOE_ITEM_SHARED | (ns > 1 ? MOE_ITEM_SPLIT : 0));
+    }
+    if (lane == 0) list[0] = tot + ns;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_group_few(const int32_t *__restrict__ ids, int P, int E, int T, int shared,
+                                                   int BT, int32_t *__restrict__ counts,
+                                                   int32_t *__restrict__ offsets, int32_t *__restrict__ perm,
+                                                   int32_t *__restrict__ inv, int32_t *__restrict__ items,
+                                                   const float *__restrict__ x, int n_xblocks,
+                                                   uint32_t *__restrict__ xq, float *__restrict__ xd, int BT2,
+                                                   int32_t *__restrict__ items2) {
+  if (blockIdx.x > 0) {
+    const int b0 = (blockIdx.x - 1) * MOE_GF_QBLOCKS;
+    const int nb = n_xblocks - b0 < MOE_GF_QBLOCKS ? n_xblocks - b0 : MOE_GF_QBLOCKS;
+    if (nb > 0) stage_quant(x + (size_t)b0 * MOE_QK, nb, xq + (size_t)b0 * MOE_XSW, xd + b0, threadIdx.x, 256);
+    return;
+  }
+  if (threadIdx.x >= 64) return;
+  if (P <= 64)
+    group_one_wave<1>(ids, P, E, T, shared, BT, counts, offsets, perm, inv, items, BT2, items2);
+  else
+    group_one_wave<2>(ids, P, E, T, shared, BT, counts, offsets, perm, inv, items, BT2, items2);
+}
+
+// ---------------------------------------------------------------------------
 // out[t][c] = ((y[r(t,0)] + y[r(t,1)]) + ...) + y[P+t]   (or per slot), with
 // r(t,s) = inv[t*k+s] (grouped rows) or t*k+s when inv is NULL (decode: the
 // y row of slot s is s).  The slot order is the reference's pairwise ADD

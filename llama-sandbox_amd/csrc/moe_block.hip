@@ -797,9 +797,14 @@ extern "C" moe_status moe_group(moe_ctx *c, const int32_t *ids, int T, int k, in
   HIPC(c, hipSetDevice(c->device));
   {
     prof_scope ps(c, K_GROUP, (hipStream_t)stream, true);
-    hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, T, 0, 1, counts,
-                       offsets, perm, inv, (int32_t *)nullptr, (const float *)nullptr, 0, (uint32_t *)nullptr,
-                       (float *)nullptr, 0, (int32_t *)nullptr);
+    if ((long)T * k <= MOE_GF_PAIRS)
+      hipLaunchKernelGGL(k_group_few, dim3(1), dim3(256), 0, (hipStream_t)stream, ids, T * k, E, T, 0, 1,
+                         counts, offsets, perm, inv, (int32_t *)nullptr, (const float *)nullptr, 0,
+                         (uint32_t *)nullptr, (float *)nullptr, 0, (int32_t *)nullptr);
+    else
+      hipLaunchKernelGGL(k_group, dim3(1), dim3(1024), 0, (hipStream_t)stream, ids, T * k, E, T, 0, 1, counts,
+                         offsets, perm, inv, (int32_t *)nullptr, (const float *)nullptr, 0, (uint32_t *)nullptr,
+                         (float *)nullptr, 0, (int32_t *)nullptr);
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
@@ -903,9 +908,15 @@ static moe_status forward_grouped(moe_ctx *c, dev_layer &L, work_bufs &s, const 
   const int n_xblocks = T * (H / MOE_QK);
   {
     prof_scope pgr(c, K_GROUP, st, s.timed);
-    hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
-                       shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, BT2,
-                       (o2 || sk) ? items16 : (int32_t *)nullptr);
+    // up to 128 pairs: the one-wave ballot grouping (no per-expert counts: nothing downstream reads them)
+    if (P <= MOE_GF_PAIRS)
+      hipLaunchKernelGGL(k_group_few, dim3(1 + ceil_div(n_xblocks, MOE_GF_QBLOCKS)), dim3(256), 0, st,
+                         ids, P, E, T, shared, BT, (int32_t *)nullptr, (int32_t *)nullptr, perm, inv, items, x,
+                         n_xblocks, s.xq, s.xd, BT2, (o2 || sk) ? items16 : (int32_t *)nullptr);
+    else
+      hipLaunchKernelGGL(k_group, dim3(1 + ceil_div(n_xblocks, MOE_GROUP_QBLOCKS)), dim3(1024), 0, st, ids, P, E, T,
+                         shared, BT, counts, offsets, perm, inv, items, x, n_xblocks, s.xq, s.xd, BT2,
+                         (o2 || sk) ? items16 : (int32_t *)nullptr);
   }
   const int cap = group_item_cap(T, k, E, BT);
   {

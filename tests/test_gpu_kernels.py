@@ -124,8 +124,13 @@ def test_route_matches_oracle(blk, torch_dev, oracle, mode, E, k, T, bias):
 
 # P = 8800 (T = 1100): more than 8 steps of 64 pairs per wave, past the ids
 # k_group keeps in registers
-# P <= 64 takes k_group's one-wave path: P = 8, 12, 32, 64, and E = 100 (not a multiple of 64)
+# P <= 128 takes the one-wave ballot grouping (k_group_few), one or two pairs per lane: P = 8, 12, 24,
+# 32, 48, 64, 65, 80, 128, with E = 100 (not a multiple of 64) and E = 16, 32 (fewer experts than pairs:
+# the per-expert loop runs on part of the wave); P = 250 and up take k_group; E = 1024 uses all 10 id bits
 @pytest.mark.parametrize("T,k,E,zipf", [(1, 8, 256, False), (4, 8, 256, True), (8, 8, 256, True), (4, 6, 100, False),
+                                        (13, 5, 100, True), (16, 8, 256, True), (8, 16, 1024, False), (25, 10, 1024, False),
+                                        (12, 4, 16, True), (20, 4, 32, False),
+                                        (16, 16, 1024, True), (32, 8, 256, True), (32, 8, 256, False),
                                         (64, 8, 256, True),
                                         (512, 8, 256, True), (512, 8, 256, False), (3, 4, 32, False),
                                         (1100, 8, 256, True), (1100, 8, 256, False)])
@@ -147,7 +152,8 @@ def test_group_bit_exact(blk, torch_dev, oracle, T, k, E, zipf):
         np.testing.assert_array_equal(t.cpu().numpy(), g[name], err_msg=name)
 
 
-@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32), (6, 8, 100), (1100, 8, 256)])
+@pytest.mark.parametrize("T,k,E", [(300, 8, 256), (5, 4, 32), (6, 8, 100), (12, 8, 256), (8, 16, 1024),
+                                   (20, 8, 256), (1100, 8, 256)])
 def test_group_drops_out_of_range_ids(blk, torch_dev, T, k, E):
     """Out-of-range ids get no grouped row (inv = -1); the valid pairs keep
     ascending pair order within each expert (checked against a stable sort)."""
