@@ -37,7 +37,8 @@ def assert_rms_close(got, ref, tol=TOL, what=""):
     r = rms(ref[fin])
     err = float(np.max(np.abs(got[fin] - ref[fin])))
     nf = int(ref.size - fin.sum())
-    say(f"{what} rms(ref)={r:.4e} max|diff|={err:.3e} ratio={err / r:.3e}" + (f" non-finite={nf}" if nf else ""))
+    ratio = err / r if r > 0 else (0.0 if err == 0 else float("inf"))  # an all-zero reference row must be met exactly
+    say(f"{what} rms(ref)={r:.4e} max|diff|={err:.3e} ratio={ratio:.3e}" + (f" non-finite={nf}" if nf else ""))
     assert err <= tol * r, f"{what}: max|diff| {err:.3e} > {tol} * rms {r:.3e}"
 
 

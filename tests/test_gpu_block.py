@@ -280,6 +280,58 @@ def test_c4_prefill_chunk(blk, torch_dev, oracle, v3, zipf):
     check_block(oracle, oracle_layer(oracle, v3, 202, 2, ids), blk, v3, x, ids, wts, got, "C4")
 
 
+@pytest.mark.slow
+@pytest.mark.parametrize("which, T", [("c1", 3), ("c1", 12), ("c1", 40), ("v3", 4), ("v3", 16), ("v3", 64)])
+def test_out_of_range_ids_contribute_nothing(request, blk, torch_dev, oracle, which, T):
+    """Pairs whose expert id is out of range (-1 or E) belong to no work item:
+    their per-slot rows are exactly 0 and they add nothing to the slot sum;
+    token 0 has every pair out of range (its output is exactly 0 on C1, the
+    shared expert's row alone on V3).  Every down path runs: the pairs path
+    with its fused slot combine (T = 3, 4), 8-row octet items (C1 T=12, V3
+    T=16), 16-row items (C1 T=40) and the stacked kernels' 32-row items (V3
+    T=64).  The yardstick is check_block on the oracle with the original
+    (valid) ids and the dropped pairs' router weights set to 0, the GPU's h
+    taps standing in for the kept pairs and the shared expert (the oracle's
+    own h for the dropped pairs, which the GPU never computes)."""
+    from parity import Taps
+    shape = request.getfixturevalue(which)
+    layer, seed = (1, 101) if which == "c1" else (2, 202)
+    E, k, F = shape.n_expert, shape.n_used, shape.ffn
+    x, lg = wl.make_inputs(shape, T, 300 + T, zipf=True)
+    ids, wts = oracle.route(lg, k, shape.route_mode, norm=True)
+    rng = np.random.default_rng(T)
+    drop = rng.random(ids.shape) < 0.15
+    drop[0, :] = True
+    bad = ids.copy()
+    bad[drop] = np.where(rng.random(int(drop.sum())) < 0.5, -1, E).astype(np.int32)
+    wts0 = wts.copy()
+    wts0[drop] = 0.0
+    say(which, "T", T, "out-of-range pairs", int(drop.sum()), "of", ids.size)
+    # grouped row of each kept pair: ascending expert, then pair order
+    flat, kept = bad.ravel(), ~drop.ravel()
+    order = np.nonzero(kept)[0][np.argsort(flat[kept], kind="stable")]
+    row_of = np.full(T * k, -1)
+    row_of[order] = np.arange(len(order))
+    L = oracle_layer(oracle, shape, seed, layer, ids)
+    ref = L.forward(x, ids, wts0, n_threads=16, taps=True)
+
+    def taps(with_shared):  # the last forward's h rows: grouped rows, then the shared expert's from row T*k
+        n = T * k + (T if with_shared else 0)
+        rows = blk.debug_last_h(n * F).reshape(n, F)
+        h = ref["h"].copy()
+        for p in np.nonzero(kept)[0]:
+            h[p // k, p % k] = rows[row_of[p]]
+        return Taps(h, rows[T * k:] if with_shared else None)
+
+    ps_dev = run_block(blk, torch_dev, layer, x, bad, wts, flags=mb.MOE_FWD_PER_SLOT)
+    assert np.all(ps_dev[drop] == 0.0)
+    check_block(oracle, L, taps(False), shape, x, ids, wts0, ps_dev, f"{which} T{T} per-slot", per_slot=True)
+    out_dev = run_block(blk, torch_dev, layer, x, bad, wts)
+    if not shape.has_shared:
+        assert np.all(out_dev[0] == 0.0)
+    check_block(oracle, L, taps(shape.has_shared), shape, x, ids, wts0, out_dev, f"{which} T{T}")
+
+
 @pytest.mark.parametrize("T", [16, 64])
 def test_graph_replay_grouped(blk, torch_dev, oracle, v3, T):
     """A grouped call captured in a graph (T=16: k_gate_up_o on the 8-row items;
