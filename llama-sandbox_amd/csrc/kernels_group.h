@@ -346,7 +346,11 @@ __device__ __forceinline__ void group_one_wave(const int32_t *__restrict__ ids, 
       n[i] = ok[i] && before[i] == 0 ? (cnt[i] + bt - 1) / bt : 0;  // first pair of its expert
       base[i] = 0;
     }
-    const int nbits = gf_bits((P + bt - 1) / bt);
+    bool big = false;  // an expert of more than one item on this lane
+#pragma unroll
+    for (int i = 0; i < NPL; i++) big |= n[i] > 1;
+    // counts of 0 or 1 everywhere (the common case): one bit; else every bit a count can have
+    const int nbits = __ballot(big) ? gf_bits((P + bt - 1) / bt) : 1;
     for (int b = 0; b < nbits; b++) {
 #pragma unroll
       for (int c = 0; c < NPL; c++) {
