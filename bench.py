@@ -62,6 +62,9 @@ def parse():
                          "that configuration (C1 decode, C3 T=4/16/64 Zipf, C4 T=512 uniform and Zipf, C5 40-layer "
                          "graph); boundary: V3 decode calls through the host-buffer split interface; server: "
                          "moe-server protocol v2 requests on a V3-shaped GGUF model")
+    ap.add_argument("--timeline", type=int, default=0,
+                    help="only run this many eager V3 decode calls with the per-wave timeline on "
+                         "(moe_debug_set_timeline) and print one JSON line of its statistics, then exit")
     ap.add_argument("--copy-mib", type=int, default=0,
                     help="only run a plain device-to-device copy of this many MiB three times (the reference "
                          "workload for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE), then exit")
@@ -642,6 +645,82 @@ def trace_gaps(path: str, n_layers: int = 40):
     print(json.dumps(line), flush=True)
 
 
+def bench_timeline(args):
+    """Per-wave timeline of eager V3 decode calls (k_gate_up_bal2 then
+    k_down_dec): the device's 100 MHz clock stamped at each wave's entry, K-loop
+    end and exit.  Each sample is the last of 8 calls launched back to back (the
+    layers cycled, steady state, as in the timed graph), summarised relative to
+    its first gate/up wave entry; the line gives the median over the samples.
+    XCD = workgroup % 8 (the dispatcher deals a 1-D grid's workgroups
+    round-robin over the 8 XCDs)."""
+    import numpy as np
+    import torch
+
+    import moe_block as mb
+    import workloads as wl
+
+    assert torch.cuda.is_available(), "bench.py needs a ROCm GPU"
+    dev = torch.device("cuda:0")
+    sh, NL, n = wl.V3, args.layers, args.timeline
+    blk = mb.MoeBlock(0)
+    for layer in range(NL):
+        blk.generate_layer(layer, sh, seed=args.seed)
+    x_np, lg_np = wl.make_inputs(sh, n, args.seed + 1)
+    x = torch.from_numpy(x_np).to(dev)
+    logits = torch.from_numpy(lg_np).to(dev)
+    ids = torch.empty((n, sh.n_used), dtype=torch.int32, device=dev)
+    wts = torch.empty((n, sh.n_used), dtype=torch.float32, device=dev)
+    blk.route(logits, sh.n_used, sh.route_mode, sh.norm, sh.scale, ids, wts)
+    out = torch.empty((n, sh.hidden), dtype=torch.float32, device=dev)
+    blk.reserve(sh, 1)
+    for i in range(4):  # warm up
+        blk.forward(i % NL, x[i:i + 1], ids[i:i + 1], wts[i:i + 1], out[i:i + 1])
+    torch.cuda.synchronize()
+    blk.set_timeline(True)
+    us = 0.01  # one tick of the 100 MHz clock
+    calls = []
+    S = sh.n_used + 1
+    for i in range(n):
+        for j in range(8):
+            q = (8 * i + j) % n
+            blk.forward(q % NL, x[q:q + 1], ids[q:q + 1], wts[q:q + 1], out[q:q + 1])
+        torch.cuda.synchronize()
+        gu, dn = blk.read_timeline()
+        assert len(gu) and len(dn), "the timeline needs the k_gate_up_bal2 decode path"
+        t0 = int(gu[:, 0].min())
+        g = (gu.astype(np.int64) - t0) * us
+        d = (dn.astype(np.int64) - t0) * us
+        gwg = g[:, 2].reshape(-1, 9).max(axis=1)  # a workgroup ends with its last wave
+        dwg = d[:, 2].reshape(-1, S).max(axis=1)
+        xcd = np.arange(len(gwg)) % 8
+        c = {
+            "gate_up_entry_max": float(g[:, 0].max()),
+            "gate_up_loop_end": [float(np.percentile(g[:, 1], q)) for q in (10, 50, 90, 100)],
+            "gate_up_wg_end": [float(np.percentile(gwg, q)) for q in (10, 50, 90, 100)],
+            "gate_up_xcd_median_end": [float(np.median(gwg[xcd == j])) for j in range(8)],
+            "down_first_entry": float(d[:, 0].min()),
+            "gap_gate_up_end_to_down_entry": float(d[:, 0].min() - g[:, 2].max()),
+            "down_entry_p50_max": [float(np.percentile(d[:, 0], 50)), float(d[:, 0].max())],
+            "down_loop_end": [float(np.percentile(d[:, 1], q)) for q in (10, 50, 90, 100)],
+            "down_wg_end": [float(np.percentile(dwg, q)) for q in (10, 50, 90, 100)],
+            "down_wg_end_first_256_last_192": [float(np.median(dwg[:256])), float(np.median(dwg[256:]))],
+            "span": float(d[:, 2].max()),
+        }
+        calls.append(c)
+    blk.set_timeline(False)
+
+    def med(key):
+        v = np.array([c[key] for c in calls], np.float64)
+        return np.round(np.median(v, axis=0), 2).tolist()
+
+    res = {"timeline": "V3 decode (C2), eager calls, each the last of 8 back to back", "samples": n, "unit": "us from the call's first gate/up wave "
+           "entry; lists are p10/p50/p90/max unless named otherwise; median over the calls",
+           "gate_up_workgroups": int(len(gu) // 9), "down_workgroups": int(len(dn) // S)}
+    for key in calls[0]:
+        res[key] = med(key)
+    print(json.dumps(res), flush=True)
+
+
 def main():
     args = parse()
     if args.trace_gaps:
@@ -655,6 +734,9 @@ def main():
               f"sharding of the block is design-only", file=sys.stderr)
         sys.exit(2)
 
+    if args.timeline > 0:
+        bench_timeline(args)
+        return
     if args.workload == "boundary":
         bench_boundary(args)
         return

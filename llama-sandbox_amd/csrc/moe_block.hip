@@ -111,6 +111,10 @@ struct moe_ctx {
   int inject = 0;  // bit 0: forward fails, bit 1: budget forced to 0
   bool capturing = false;
   bool taps = false;  // keep the SwiGLU output h in sc.htap (moe_debug_set_taps)
+  // per-wave timestamps of the last decode call's k_gate_up_bal2 and k_down_dec
+  // (moe_debug_set_timeline): MOE_TL_RECORDS records of 3 stamps
+  unsigned long long *tl = nullptr;
+  size_t tl_gu = 0, tl_dn = 0;  // records written by the last decode call
   prof_state prof;
   // moe_forward_host's pinned staging (x, ids, wts in; out back), grown on demand
   uint8_t *pin = nullptr;
@@ -239,6 +243,8 @@ static uint64_t layer_bytes(const moe_layer_desc *d) {
 
 // ---------------------------------------------------------------------------
 // scratch
+
+#define MOE_TL_RECORDS 8192  // debug timeline: waves of one decode call's two launches
 
 static void scratch_free(work_bufs &s) {
   void *ptrs[] = {s.hq, s.hd, s.htap, s.y, s.xq, s.xd, s.part, s.tick, s.grp, s.ids_in, s.out_buf};
@@ -434,6 +440,7 @@ extern "C" void moe_ctx_destroy(moe_ctx *c) {
       if (m.w) (void)hipFree(m.w);
   scratch_free(c->sc);
   if (c->pin) (void)hipHostFree(c->pin);
+  if (c->tl) (void)hipFree(c->tl);
   for (auto &r : c->prof.pending) {
     (void)hipEventDestroy(r.a);
     (void)hipEventDestroy(r.b);
@@ -838,6 +845,11 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, work_bufs &s, const f
   const size_t lds1 = gate_up_lds_bytes(H, 1), lds2 = down_dec_lds_bytes(F, S);
   if (S > 16 || lds1 > 65536 || lds2 > 65536)
     return forward_grouped(c, L, s, x, ids, wts, 1, out, flags, st);  // the grouped chain takes any shape
+  // the debug timeline (eager calls only): gate/up's records, then down's
+  const size_t n_dn = (size_t)(H / MOE_TILE) * S;
+  unsigned long long *tl = c->tl && !c->capturing && n_dn <= MOE_TL_RECORDS ? c->tl : nullptr;
+  c->tl_gu = 0;
+  c->tl_dn = 0;
   {
     prof_scope pg(c, K_GU_DECODE, st, s.timed);
     // the balanced kernels run one workgroup per CU: for shapes too small to
@@ -848,9 +860,12 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, work_bufs &s, const f
       launch_gate_up_decode(dim3(F / MOE_UNIT, S), st, L, x, ids, shared, s.hq, s.hd, htap);
     } else if (n_tasks % MOE_BAL_WAVES == 0 && (n_tasks / MOE_BAL_WAVES) % 4 == 0 &&
                gate_up_bal2_lds_bytes(H) <= 65536) {
+      const size_t n_gu = (size_t)n_tasks;  // 9 waves per workgroup, one task each
+      unsigned long long *tg = tl && n_gu + n_dn <= MOE_TL_RECORDS ? tl : nullptr;
       hipLaunchKernelGGL(k_gate_up_bal2, dim3(n_tasks / MOE_BAL_WAVES), dim3(64 * MOE_BAL_WAVES),
                          gate_up_bal2_lds_bytes(H), st, L.m[T_GATE].w, L.m[T_UP].w, x, ids, k, E, S, F, H, d.clamp,
-                         s.part, s.tick, s.hq, s.hd, htap);
+                         s.part, s.tick, s.hq, s.hd, htap, tg);
+      if (tg) c->tl_gu = n_gu;
     } else if (gate_up_bal_lds_bytes(H) <= 65536) {
       const int n_wg = ceil_div((long)S * (F / MOE_UNIT) * 4, MOE_BAL_WAVES);
       hipLaunchKernelGGL(k_gate_up_bal, dim3(n_wg), dim3(64 * MOE_BAL_WAVES), gate_up_bal_lds_bytes(H), st,
@@ -865,7 +880,8 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, work_bufs &s, const f
   {
     prof_scope pd(c, K_DOWN_DECODE, st, s.timed);
     hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].w, s.hq, s.hd, ids,
-                       wts, k, E, S, F, H, per_slot ? 1 : 0, out);
+                       wts, k, E, S, F, H, per_slot ? 1 : 0, out, tl ? tl + 3 * c->tl_gu : nullptr);
+    if (tl) c->tl_dn = n_dn;
   }
   HIPC(c, hipGetLastError());
   return MOE_OK;
@@ -1283,6 +1299,32 @@ extern "C" moe_status moe_prof_read(moe_ctx *c, moe_kernel_stat *stats, int cap,
 extern "C" moe_status moe_debug_set_taps(moe_ctx *c, int on) {
   if (!c) return MOE_ERR_INVALID_ARG;
   c->taps = on != 0;
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_debug_set_timeline(moe_ctx *c, int on) {
+  if (!c) return MOE_ERR_INVALID_ARG;
+  HIPC(c, hipSetDevice(c->device));
+  if (on && !c->tl) {
+    HIPC(c, hipMalloc(&c->tl, (size_t)MOE_TL_RECORDS * 3 * 8));
+  } else if (!on && c->tl) {
+    HIPC(c, hipDeviceSynchronize());
+    HIPC(c, hipFree(c->tl));
+    c->tl = nullptr;
+  }
+  c->tl_gu = c->tl_dn = 0;
+  return MOE_OK;
+}
+
+extern "C" moe_status moe_debug_read_timeline(moe_ctx *c, uint64_t *stamps, size_t cap, size_t *n_gate_up,
+                                              size_t *n_down) {
+  if (!c || !n_gate_up || !n_down || (cap && !stamps)) return MOE_ERR_INVALID_ARG;
+  const size_t n = c->tl_gu + c->tl_dn;
+  if (cap < 3 * n) return fail(c, MOE_ERR_INVALID_ARG, "moe_debug_read_timeline: %zu stamps do not fit %zu", 3 * n, cap);
+  HIPC(c, hipDeviceSynchronize());
+  if (n) HIPC(c, hipMemcpy(stamps, c->tl, n * 3 * 8, hipMemcpyDeviceToHost));
+  *n_gate_up = c->tl_gu;
+  *n_down = c->tl_dn;
   return MOE_OK;
 }
 

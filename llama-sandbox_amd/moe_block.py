@@ -42,7 +42,8 @@ EXPORTS = (
     "moe_forward_host",
     "moe_route_forward", "moe_graph_capture", "moe_graph_launch", "moe_graph_destroy",
     "moe_prof_enable", "moe_prof_read", "moe_call_stats_read", "moe_debug_set_taps",
-    "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h",
+    "moe_debug_quantize_q8_0", "moe_debug_wave_sum", "moe_debug_last_h", "moe_debug_set_timeline",
+    "moe_debug_read_timeline",
     "moe_gguf_read_layer", "moe_layer_upload_gguf",
     "moe_server_open", "moe_server_close", "moe_server_last_error", "moe_server_handle", "moe_server_listen",
     "moe_server_serve", "moe_router_logits", "moe_node_claimed", "moe_split_parse", "moe_split_compute",
@@ -212,6 +213,11 @@ def load_library(path: str | None = None):
     L.moe_debug_wave_sum.argtypes = [_vp, _vp, ctypes.c_int, _vp, _vp]
     L.moe_debug_last_h.restype = st
     L.moe_debug_last_h.argtypes = [_vp, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)]
+    L.moe_debug_set_timeline.restype = st
+    L.moe_debug_set_timeline.argtypes = [_vp, ctypes.c_int]
+    L.moe_debug_read_timeline.restype = st
+    L.moe_debug_read_timeline.argtypes = [_vp, _vp, ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t),
+                                          ctypes.POINTER(ctypes.c_size_t)]
     L.moe_gguf_read_layer.restype = st
     L.moe_gguf_read_layer.argtypes = [ctypes.c_char_p, ctypes.c_int, ctypes.POINTER(GgufLayer), ctypes.c_char_p,
                                       ctypes.c_size_t]
@@ -586,6 +592,19 @@ class MoeBlock:
         n = ctypes.c_size_t()
         self._check(self.lib.moe_debug_last_h(self.h, buf.ctypes.data, cap, ctypes.byref(n)), "moe_debug_last_h")
         return buf[: n.value]
+
+    def set_timeline(self, on: bool = True):
+        self._check(self.lib.moe_debug_set_timeline(self.h, int(on)), "moe_debug_set_timeline")
+
+    def read_timeline(self):
+        """The last eager decode call's per-wave stamps (100 MHz clock ticks):
+        (gate_up [n, 3], down [n, 3]) uint64, columns entry / K-loop end / exit."""
+        buf = np.empty(3 * 8192, np.uint64)
+        ng, nd = ctypes.c_size_t(), ctypes.c_size_t()
+        self._check(self.lib.moe_debug_read_timeline(self.h, buf.ctypes.data, buf.size, ctypes.byref(ng),
+                                                     ctypes.byref(nd)), "moe_debug_read_timeline")
+        st = buf[: 3 * (ng.value + nd.value)].reshape(-1, 3)
+        return st[: ng.value].copy(), st[ng.value:].copy()
 
 
 class MoeServer:

@@ -203,6 +203,32 @@ def test_c2_decode_per_slot_and_no_shared(blk, torch_dev, oracle, v3):
     np.testing.assert_array_equal(ns[0].view(np.int32), acc.view(np.int32))
 
 
+def test_decode_timeline(blk, torch_dev, oracle, v3):
+    """The debug timeline of a V3 decode call: one record per wave of the two
+    launches (256 x 9 gate/up, 448 x 9 down), each entry <= K-loop end <=
+    exit, down entering after gate/up's last exit; the output is the same
+    bits with the timeline on and off."""
+    x, lg = wl.make_inputs(v3, 1, 8)
+    ids, wts = oracle.route(lg, v3.n_used, v3.route_mode, norm=True)
+    say("C2 decode timeline")
+    off = run_block(blk, torch_dev, 2, x, ids, wts)
+    blk.set_timeline(True)
+    try:
+        on = run_block(blk, torch_dev, 2, x, ids, wts)
+        gu, dn = blk.read_timeline()
+    finally:
+        blk.set_timeline(False)
+    assert np.array_equal(on.view(np.uint32), off.view(np.uint32))
+    S = v3.n_used + 1
+    assert gu.shape == (v3.ffn // 32 * S * 4, 3) and dn.shape == (v3.hidden // 16 * S, 3)
+    for st in (gu, dn):
+        assert np.all(st[:, 0] <= st[:, 1]) and np.all(st[:, 1] <= st[:, 2]) and np.all(st[:, 0] > 0)
+    assert int(dn[:, 0].min()) >= int(gu[:, 2].max())
+    span_us = (int(dn[:, 2].max()) - int(gu[:, 0].min())) * 0.01
+    say(f"decode span {span_us:.1f} us")
+    assert 5.0 < span_us < 1000.0
+
+
 def test_c2_route_forward_ids_bit_exact(blk, torch_dev, oracle, v3):
     torch, dev = torch_dev
     x, lg = wl.make_inputs(v3, 1, 3)
