@@ -694,12 +694,12 @@ void k_gate_up(
 // Nothing waits.  grid ceil(S*U*4 / MOE_BAL_WAVES), 64*MOE_BAL_WAVES threads.
 #define MOE_BAL_WAVES 9
 
-// Debug timeline (tl != NULL, off in production): per wave, three stamps of
-// the device's constant 100 MHz clock -- entry, end of its K loop, exit --
-// at record rec: tl[3 * rec + 0 .. 2].  Lane 0 stores them with vector stores.
+// Debug timeline (the TL instances of the decode kernels; production runs
+// TL = false, the same code as without it): per wave, three stamps of the
+// device's constant 100 MHz clock -- entry, end of its K loop, exit -- at
+// record rec: tl[3 * rec + 0 .. 2].  Lane 0 stores them with vector stores.
 __device__ __forceinline__ void tl_mark(unsigned long long *tl, int rec, unsigned long long t_in,
                                         unsigned long long t_loop) {
-  if (!tl) return;
   const unsigned long long t_out = wall_clock64();
   if ((threadIdx.x & 63) == 0) {
     tl[3 * (size_t)rec + 0] = t_in;
@@ -779,12 +779,13 @@ static inline size_t gate_up_bal_lds_bytes(int H) {
 // grid G, 64*MOE_BAL_WAVES threads, LDS gate_up_bal2_lds_bytes(H).
 #define MOE_BAL2_RING 8
 
+template <bool TL>
 __global__ __launch_bounds__(64 * MOE_BAL_WAVES) void k_gate_up_bal2(
     const uint8_t *__restrict__ w_g, const uint8_t *__restrict__ w_u, const float *__restrict__ x,
     const int32_t *__restrict__ ids, int k, int E, int S, int F, int H, float clamp, float *__restrict__ part,
     int *__restrict__ tick, uint32_t *__restrict__ hs, float *__restrict__ hd, float *__restrict__ htap,
     unsigned long long *__restrict__ tl) {
-  const unsigned long long t_in = tl ? wall_clock64() : 0ull;
+  const unsigned long long t_in = TL ? wall_clock64() : 0ull;
   extern __shared__ __align__(16) uint32_t lds[];
   const int NQ = H / 128, NQ4 = moe_nq4(NQ), KB = H / MOE_QK, U = F / MOE_UNIT, tiles = F / MOE_TILE;
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -821,7 +822,7 @@ __global__ __launch_bounds__(64 * MOE_BAL_WAVES) void k_gate_up_bal2(
   f32x4_t acc[1][1];
   if (local) kloop_any<1, 1, MOE_BAL_RING>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
   else kloop_any<1, 1, MOE_BAL2_RING>(ring8, ws, 0, NQ, bs, xs, dy, lane, acc);
-  const unsigned long long t_loop = tl ? wall_clock64() : 0ull;
+  const unsigned long long t_loop = TL ? wall_clock64() : 0ull;
   const int gb = lane >> 4, tp = (lane >> 3) & 1;
   if (local) {
 #pragma unroll
@@ -870,7 +871,7 @@ __global__ __launch_bounds__(64 * MOE_BAL_WAVES) void k_gate_up_bal2(
     h_unit_store(h, true, hs + ((size_t)s2 * U + u2) * MOE_XSW, hd + (size_t)s2 * U + u2, lane);
     if (htap) htap[(size_t)s2 * F + (size_t)u2 * MOE_UNIT + j] = h;
   }
-  tl_mark(tl, blockIdx.x * MOE_BAL_WAVES + wave, t_in, t_loop);
+  if (TL) tl_mark(tl, blockIdx.x * MOE_BAL_WAVES + wave, t_in, t_loop);
 }
 
 static inline size_t gate_up_bal2_lds_bytes(int H) {
@@ -886,11 +887,12 @@ static inline size_t gate_up_bal2_lds_bytes(int H) {
 // y_s (the MUL node of the reference's split) instead.
 // grid H/16, 64*S threads.  LDS: per wave [zero 4][xs F/32*16][dy F/32]
 // dwords, then ys[S][16].
+template <bool TL>
 __global__ __launch_bounds__(1024) void k_down_dec(
     const uint8_t *__restrict__ w_d, const uint32_t *__restrict__ hs, const float *__restrict__ hd,
     const int32_t *__restrict__ ids, const float *__restrict__ wts, int k, int E,
     int S, int F, int H, int per_slot, float *__restrict__ out, unsigned long long *__restrict__ tl) {
-  const unsigned long long t_in = tl ? wall_clock64() : 0ull;
+  const unsigned long long t_in = TL ? wall_clock64() : 0ull;
   extern __shared__ __align__(16) uint32_t lds[];
   const int NQ = F / 128, NQ4 = moe_nq4(NQ), tiles = H / MOE_TILE, U = F / MOE_UNIT;
   const int nb = F / MOE_QK, wave_words = 4 + nb * (MOE_XSW + 1);
@@ -923,7 +925,7 @@ __global__ __launch_bounds__(1024) void k_down_dec(
   const bsel bs[1] = {make_bsel(lane, 4, 4, 0, 0, true, false, 0)};
   f32x4_t acc[1][1];
   kloop_any<1, 1, 4>(ring, ws, 0, NQ, bs, xs, dy, lane, acc);
-  const unsigned long long t_loop = tl ? wall_clock64() : 0ull;
+  const unsigned long long t_loop = TL ? wall_clock64() : 0ull;
   const int gb = lane >> 4;
   const float wt = s < k ? wts[s] : 1.0f;
   float v[4];
@@ -938,7 +940,7 @@ __global__ __launch_bounds__(1024) void k_down_dec(
     if ((lane & 15) == 0)
 #pragma unroll
       for (int r = 0; r < 4; r++) out[(size_t)s * H + row0 + r] = v[r];
-    tl_mark(tl, blockIdx.x * S + s, t_in, t_loop);
+    if (TL) tl_mark(tl, blockIdx.x * S + s, t_in, t_loop);
     return;
   }
   if ((lane & 15) == 0)
@@ -950,7 +952,7 @@ __global__ __launch_bounds__(1024) void k_down_dec(
     for (int q = 1; q < S; q++) o = __fadd_rn(o, ys[q * MOE_TILE + threadIdx.x]);
     out[(size_t)tile * MOE_TILE + threadIdx.x] = o;
   }
-  tl_mark(tl, blockIdx.x * S + s, t_in, t_loop);
+  if (TL) tl_mark(tl, blockIdx.x * S + s, t_in, t_loop);
 }
 
 // LDS bytes of the kernels.

@@ -862,9 +862,9 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, work_bufs &s, const f
                gate_up_bal2_lds_bytes(H) <= 65536) {
       const size_t n_gu = (size_t)n_tasks;  // 9 waves per workgroup, one task each
       unsigned long long *tg = tl && n_gu + n_dn <= MOE_TL_RECORDS ? tl : nullptr;
-      hipLaunchKernelGGL(k_gate_up_bal2, dim3(n_tasks / MOE_BAL_WAVES), dim3(64 * MOE_BAL_WAVES),
-                         gate_up_bal2_lds_bytes(H), st, L.m[T_GATE].w, L.m[T_UP].w, x, ids, k, E, S, F, H, d.clamp,
-                         s.part, s.tick, s.hq, s.hd, htap, tg);
+      hipLaunchKernelGGL(tg ? k_gate_up_bal2<true> : k_gate_up_bal2<false>, dim3(n_tasks / MOE_BAL_WAVES),
+                         dim3(64 * MOE_BAL_WAVES), gate_up_bal2_lds_bytes(H), st, L.m[T_GATE].w, L.m[T_UP].w, x, ids, k,
+                         E, S, F, H, d.clamp, s.part, s.tick, s.hq, s.hd, htap, tg);
       if (tg) c->tl_gu = n_gu;
     } else if (gate_up_bal_lds_bytes(H) <= 65536) {
       const int n_wg = ceil_div((long)S * (F / MOE_UNIT) * 4, MOE_BAL_WAVES);
@@ -879,8 +879,9 @@ static moe_status forward_decode(moe_ctx *c, dev_layer &L, work_bufs &s, const f
   s.last_F = F;
   {
     prof_scope pd(c, K_DOWN_DECODE, st, s.timed);
-    hipLaunchKernelGGL(k_down_dec, dim3(H / MOE_TILE), dim3(64 * S), lds2, st, L.m[T_DOWN].w, s.hq, s.hd, ids,
-                       wts, k, E, S, F, H, per_slot ? 1 : 0, out, tl ? tl + 3 * c->tl_gu : nullptr);
+    hipLaunchKernelGGL(tl ? k_down_dec<true> : k_down_dec<false>, dim3(H / MOE_TILE), dim3(64 * S), lds2, st,
+                       L.m[T_DOWN].w, s.hq, s.hd, ids, wts, k, E, S, F, H, per_slot ? 1 : 0, out,
+                       tl ? tl + 3 * c->tl_gu : nullptr);
     if (tl) c->tl_dn = n_dn;
   }
   HIPC(c, hipGetLastError());
