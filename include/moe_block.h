@@ -514,8 +514,8 @@ moe_status moe_debug_last_h(moe_ctx *ctx, float *h_host, size_t cap, size_t *n);
  * reference; a profiling aid).  While on, every eager T == 1 moe_forward
  * that runs k_gate_up_bal2 and k_down_dec stamps, for each of their waves,
  * three readings of the device's constant 100 MHz clock: entry, end of the
- * wave's K loop, exit.  moe_debug_read_timeline copies the last call's
- * stamps: n_gate_up records of k_gate_up_bal2 (record = workgroup * 9 +
+ * wave's K loop, exit.  moe_debug_read_timeline copies the stamps of the
+ * last such call: n_gate_up records of k_gate_up_bal2 (record = workgroup * 9 +
  * wave), then n_down of k_down_dec (record = 16-row tile * S + slot wave),
  * 3 uint64 each; cap counts uint64s.  Off by default; turning it on
  * allocates a device buffer of 8192 records. */
