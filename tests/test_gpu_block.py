@@ -307,6 +307,33 @@ def test_c4_prefill_chunk(blk, torch_dev, oracle, v3, zipf):
 
 
 @pytest.mark.slow
+@pytest.mark.parametrize("which, zipf", [("V4P", False), ("V4P", True), ("F1536", False)])
+def test_prefill_bench_shapes(blk, torch_dev, oracle, which, zipf):
+    """T=512 on the two prefill shapes bench.py measures beyond the
+    configurations, at their full size, every token against the oracle:
+    the reference's DeepSeek-V4-Pro layer (hip-moe/README.md:280-286:
+    7168 -> 3072, 384 experts, top-6 sqrt(softplus) routing renormalised
+    and scaled by 2.5, SwiGLU clamped at 10, one shared expert;
+    k_gate_up_sk<56> over 24 slices of F, k_down_sk<24>), uniform and
+    Zipf-routed, and the V3 layer with 1536-wide experts (12 slices of F,
+    k_down_sk<12>)."""
+    shape = wl.V4P if which == "V4P" else wl.V3F1536
+    lid = 60 if which == "V4P" else 61
+    T = 512
+    blk.generate_layer(lid, shape, seed=610 + lid)
+    try:
+        x, lg = wl.make_inputs(shape, T, 95 + int(zipf), zipf=zipf)
+        ids, wts = oracle.route(lg, shape.n_used, shape.route_mode, norm=shape.norm, scale=shape.scale)
+        g = oracle.group(ids, shape.n_expert)
+        say(f"{which} T=512 zipf {zipf}: {g['distinct']} experts, the hottest with {int(g['counts'].max())} rows")
+        got = run_block(blk, torch_dev, lid, x, ids, wts)
+        check_block(oracle, oracle_layer(oracle, shape, 610 + lid, lid, ids), blk, shape, x, ids, wts, got,
+                    f"{which} T=512" + (" Zipf" if zipf else ""))
+    finally:
+        blk.release_layer(lid)
+
+
+@pytest.mark.slow
 @pytest.mark.parametrize("which, T", [("c1", 3), ("c1", 12), ("c1", 40), ("v3", 4), ("v3", 16), ("v3", 64)])
 def test_out_of_range_ids_contribute_nothing(request, blk, torch_dev, oracle, which, T):
     """Pairs whose expert id is out of range (-1 or E) belong to no work item:
