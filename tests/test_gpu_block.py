@@ -101,6 +101,52 @@ def test_forward_host_staging_grows_and_shrinks(blk, torch_dev, oracle, c1):
         assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (T, flags)
 
 
+def test_forward_host_decode_calls_across_buffer_moves(blk, torch_dev, oracle):
+    """Decode calls (T = 1) through the host boundary, in a row and across
+    the events that move the buffers they use: new inputs, the other flags,
+    a larger call that regrows the pinned staging and the scratch, the layer
+    released and generated again from another seed (new weights at new
+    addresses), and the taps switched off and on.  Every call must equal the
+    device-resident forward on the same inputs, bit for bit, and the
+    regenerated layer the oracle on its new weights."""
+    shape = wl.C1
+    lid = 71
+    blk.generate_layer(lid, shape, seed=171)
+    try:
+        def check(i, flags=0, seed_note=""):
+            x, lg = wl.make_inputs(shape, 1, 500 + i)
+            ids, wts = oracle.route(lg, shape.n_used, shape.route_mode, norm=True)
+            got = blk.forward_host(lid, x, ids, wts, flags=flags)
+            ref = run_block(blk, torch_dev, lid, x, ids, wts, flags)
+            assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (i, flags, seed_note)
+            return got, x, ids, wts
+
+        for i in range(4):  # first call captures, the others replay
+            check(i)
+        check(4, mb.MOE_FWD_PER_SLOT)
+        check(5)
+        big_T = 96  # more tokens than any earlier call: the staging and the scratch grow
+        x, lg = wl.make_inputs(shape, big_T, 510)
+        ids, wts = oracle.route(lg, shape.n_used, shape.route_mode, norm=True)
+        got = blk.forward_host(lid, x, ids, wts)
+        assert np.array_equal(got.view(np.uint32), run_block(blk, torch_dev, lid, x, ids, wts).view(np.uint32))
+        check(6)
+        check(7, mb.MOE_FWD_PER_SLOT)
+        blk.release_layer(lid)
+        blk.generate_layer(lid, shape, seed=172)
+        got, x, ids, wts = check(8, seed_note="regenerated")
+        assert_rms_close(got, oracle_layer(oracle, shape, 172, lid, ids).forward(x, ids, wts)["out"],
+                         what="host graph after the layer was generated again")
+        blk.set_taps(False)
+        try:
+            check(9)
+        finally:
+            blk.set_taps(True)
+        check(10)
+    finally:
+        blk.release_layer(lid)
+
+
 def test_c1_multi_token_grouped(blk, torch_dev, oracle, c1):
     x, lg = wl.make_inputs(c1, 6, 21, zipf=True)
     ids, wts = oracle.route(lg, c1.n_used, c1.route_mode, norm=True)
