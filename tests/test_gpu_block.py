@@ -559,31 +559,42 @@ def test_grouping_limits(blk, torch_dev, oracle, H, F, E, k, T, route):
 # ---- seeded random shapes: H, F, E, top-k, T, shared, clamp and routing drawn at random -----
 
 def _random_case(i):
-    rng = np.random.default_rng(8100 + i)
+    rng = np.random.default_rng(9100 + i)
     H = int(rng.choice([1024, 2048, 3072, 4096, 5120, 6144, 7168]))
     F = int(rng.choice([512, 768, 1024, 1536, 2048, 3072]))
-    E = int(rng.choice([8, 16, 32, 64, 128, 256]))
+    E = int(rng.choice([8, 16, 32, 64, 128, 256, 384]))
     k = int(rng.integers(1, min(8, E) + 1))
-    T = int(rng.choice([1, 2, 3, 4, 5, 8, 13, 16, 31, 40, 64, 100, 200]))
-    return H, F, E, k, T, bool(rng.integers(0, 2)), float(rng.choice([0.0, 0.0, 2.0, 6.0])), \
-        int(rng.choice([wl.ROUTE_SOFTMAX, wl.ROUTE_SIGMOID, wl.ROUTE_SQRT_SOFTPLUS]))
+    T = int(rng.choice([1, 1, 2, 3, 4, 5, 7, 8, 9, 13, 16, 17, 31, 33, 40, 64, 65, 100, 128, 129, 200, 256, 512]))
+    if T * k > 2048 and H * F > 4096 * 2048:
+        T = max(1, 2048 // k)  # keeps the oracle's share of a case to seconds
+    sh = bool(rng.integers(0, 2))
+    clamp = float(rng.choice([0.0, 0.0, 2.0, 6.0, 10.0]))
+    route = int(rng.choice([wl.ROUTE_SOFTMAX, wl.ROUTE_SIGMOID, wl.ROUTE_SQRT_SOFTPLUS]))
+    per_slot = bool(rng.integers(0, 4) == 0)
+    zipf = bool(rng.integers(0, 3) == 0)
+    return H, F, E, k, T, sh, clamp, route, per_slot, zipf
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("case", range(40))
+@pytest.mark.parametrize("case", range(80))
 def test_random_shapes(blk, torch_dev, oracle, case):
-    """Shapes off every curated list, against the oracle with the same gates."""
-    H, F, E, k, T, sh, clamp, route = _random_case(case)
+    """Shapes off every curated list (hidden 1024-7168, expert FFN 512-3072,
+    8-384 experts, top-1 to top-8, 1-512 tokens, any routing, clamps up to
+    10, uniform or Zipf-skewed routing, combined or per-slot output), against
+    the oracle with the same gates.  A wider run of the same generator (800
+    cases) passed once on the GPU; these are its first 80."""
+    H, F, E, k, T, sh, clamp, route, per_slot, zipf = _random_case(case)
     shape = wl.LayerShape(hidden=H, ffn=F, n_expert=E, n_used=k, has_shared=sh, route_mode=route, clamp=clamp)
-    say(f"random case {case}: H={H} F={F} E={E} k={k} T={T} shared={sh} clamp={clamp} route={route}")
-    lid = 600 + case
-    blk.generate_layer(lid, shape, seed=5000 + case)
+    say(f"random case {case}: H={H} F={F} E={E} k={k} T={T} shared={sh} clamp={clamp} route={route} "
+        f"per_slot={per_slot} zipf={zipf}")
+    lid = 900  # the weights of the wider run: generator keyed by (seed, layer)
+    blk.generate_layer(lid, shape, seed=7000 + case)
     try:
-        x, lg = wl.make_inputs(shape, T, 170 + case)
+        x, lg = wl.make_inputs(shape, T, 300 + case, zipf=zipf)
         ids, wts = oracle.route(lg, k, route, norm=True)
-        got = run_block(blk, torch_dev, lid, x, ids, wts)
-        check_block(oracle, oracle_layer(oracle, shape, 5000 + case, lid, ids), blk, shape, x, ids, wts, got,
-                    f"random {case}")
+        got = run_block(blk, torch_dev, lid, x, ids, wts, mb.MOE_FWD_PER_SLOT if per_slot else 0)
+        check_block(oracle, oracle_layer(oracle, shape, 7000 + case, lid, ids), blk, shape, x, ids, wts, got,
+                    f"random {case}", per_slot=per_slot)
     finally:
         blk.release_layer(lid)
 
